@@ -1,0 +1,25 @@
+"""MI355X-native MaxSim scoring (gfx950 HIP kernels behind a C ABI).
+
+Drop-in for the reference package flash_maxsim 0.1.0
+(flash_maxsim/__init__.py:1-5): the same nine callables with the same
+signatures. ``import flash_maxsim_amd as flash_maxsim`` keeps existing call
+sites unchanged.
+"""
+
+__version__ = "0.1.0"
+
+from .flash_maxsim import flash_maxsim, flash_maxsim_batched, flash_maxsim_train, maxsim_naive
+from .flash_maxsim_quant import flash_maxsim_int8, quantize_int8, dequantize_int8
+from .flash_maxsim_sparse import flash_maxsim_sparse, maxsim_sparse_naive
+
+__all__ = [
+    "flash_maxsim",
+    "flash_maxsim_batched",
+    "flash_maxsim_train",
+    "maxsim_naive",
+    "flash_maxsim_int8",
+    "quantize_int8",
+    "dequantize_int8",
+    "flash_maxsim_sparse",
+    "maxsim_sparse_naive",
+]

@@ -1,0 +1,289 @@
+// C ABI of libflashmaxsim: argument validation, workspace sizing and kernel
+// selection. Declarations and the contract live in include/fmx.h.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "../../include/fmx.h"
+#include "fmx_device.h"
+#include "fmx_kernels.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int ok() {
+  g_err.clear();
+  return FMX_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+constexpr int64_t kOffLimit = (int64_t)1 << 31;  // buffer offsets stay below 2^31
+
+// Kernel family and pass count for a forward shape.
+struct FwdPlan {
+  bool splitd;
+  int passes;
+};
+
+FwdPlan plan_fwd(int64_t Lq, int64_t d) {
+  FwdPlan p;
+  p.splitd = d > 256;
+  p.passes = p.splitd ? fmx::splitd_fwd_passes((int)Lq, (int)d) : fmx::stream_fwd_passes((int)Lq, (int)d);
+  return p;
+}
+
+size_t fwd_ws_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t d) {
+  if (Lq < 1 || d < 1 || d > FMX_MAX_D || Nq < 1 || B < 1) return 0;
+  const FwdPlan p = plan_fwd(Lq, d);
+  return p.passes > 1 ? (size_t)p.passes * (size_t)Nq * (size_t)B * sizeof(float) : 0;
+}
+
+// Checks shared by the forward entry points. esz: bytes per D element.
+int check_common(int64_t Nq, int64_t B, int64_t Lq, int64_t Ld, int64_t d, int64_t q_stride_l,
+                 int64_t d_stride_b, int64_t d_stride_l, int esz) {
+  if (Nq < 1 || B < 0 || Lq < 1 || Ld < 0 || d < 1)
+    return fail(FMX_ERR_INVALID, "invalid sizes Nq=%lld B=%lld Lq=%lld Ld=%lld d=%lld", (long long)Nq,
+                (long long)B, (long long)Lq, (long long)Ld, (long long)d);
+  if (d > FMX_MAX_D) return fail(FMX_ERR_UNSUPPORTED, "d=%lld exceeds FMX_MAX_D=%d", (long long)d, FMX_MAX_D);
+  if (q_stride_l < d || (q_stride_l & 7))
+    return fail(FMX_ERR_INVALID, "Q row stride %lld must be >= d and a multiple of 8", (long long)q_stride_l);
+  if (d_stride_l < d || (d_stride_l & 7))
+    return fail(FMX_ERR_INVALID, "D row stride %lld must be >= d and a multiple of 8", (long long)d_stride_l);
+  if (d_stride_b & 7) return fail(FMX_ERR_INVALID, "D doc stride %lld must be a multiple of 8", (long long)d_stride_b);
+  if (Nq * B >= kOffLimit) return fail(FMX_ERR_UNSUPPORTED, "Nq*B=%lld too large", (long long)(Nq * B));
+  if ((Lq + 128) * q_stride_l * 2 >= kOffLimit)
+    return fail(FMX_ERR_UNSUPPORTED, "query of %lld x %lld elements exceeds 2 GiB", (long long)Lq,
+                (long long)q_stride_l);
+  if ((Ld + 16) * d_stride_l * esz >= kOffLimit)
+    return fail(FMX_ERR_UNSUPPORTED, "doc of %lld x %lld elements exceeds 2 GiB", (long long)Ld,
+                (long long)d_stride_l);
+  return FMX_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(FMX_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* fmx_version(void) { return "0.1.0+mi355x"; }
+
+const char* fmx_last_error(void) { return g_err.c_str(); }
+
+size_t fmx_fwd_workspace_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t Ld, int64_t d) {
+  (void)Ld;
+  return fwd_ws_bytes(Nq, B, Lq, d);
+}
+
+size_t fmx_fwd_int8_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld, int64_t d) {
+  (void)Ld;
+  return fwd_ws_bytes(1, B, Lq, d);
+}
+
+int fmx_fwd(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, const void* D,
+            int64_t d_stride_b, int64_t d_stride_l, const int32_t* lengths, float* scores,
+            int64_t s_stride_n, int64_t s_stride_b, int32_t* argmax, int64_t Nq, int64_t B,
+            int64_t Lq, int64_t Ld, int64_t d, int shared_docs, void* workspace,
+            size_t workspace_bytes, void* stream) {
+  if (dtype != FMX_DTYPE_F16 && dtype != FMX_DTYPE_BF16) return fail(FMX_ERR_INVALID, "unknown dtype %d", dtype);
+  int rc = check_common(Nq, B, Lq, Ld, d, q_stride_l, d_stride_b, d_stride_l, 2);
+  if (rc) return rc;
+  if (B == 0) return ok();
+  if (!Q || !D || !scores) return fail(FMX_ERR_INVALID, "Q, D and scores must be non-null");
+  if (!aligned16(Q) || !aligned16(D)) return fail(FMX_ERR_INVALID, "Q and D must be 16-byte aligned");
+  if (Nq > 1 && (q_stride_n & 7)) return fail(FMX_ERR_INVALID, "Q query stride must be a multiple of 8");
+  const size_t need = fwd_ws_bytes(Nq, B, Lq, d);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(FMX_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+
+  fmx::FwdArgs a = {};
+  a.Q = Q;
+  a.D = D;
+  a.lengths = lengths;
+  a.scores = scores;
+  a.argmax = argmax;
+  a.partial = static_cast<float*>(workspace);
+  a.sq_n = Nq > 1 ? q_stride_n : 0;
+  a.sq_l = q_stride_l;
+  a.sd_b = d_stride_b;
+  a.sd_l = d_stride_l;
+  a.ss_n = s_stride_n;
+  a.ss_b = s_stride_b;
+  a.Nq = (int)Nq;
+  a.B = (int)B;
+  a.Lq = (int)Lq;
+  a.Lq_rows = (int)Lq;
+  a.Ld = (int)Ld;
+  a.d = (int)d;
+  a.shared_docs = shared_docs ? 1 : 0;
+  const int kind = dtype == FMX_DTYPE_BF16 ? fmx::KIND_BF16 : fmx::KIND_F16;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const hipError_t e = plan_fwd(Lq, d).splitd ? fmx::launch_splitd_fwd(kind, a, argmax != nullptr, s)
+                                              : fmx::launch_stream_fwd(kind, a, argmax != nullptr, s);
+  return hip_status(e, "fmx_fwd launch");
+}
+
+int fmx_fwd_int8(const void* Q, int64_t q_stride_l, const uint8_t* D, int64_t d_stride_b,
+                 int64_t d_stride_l, const void* scales, const void* mins, int64_t sm_stride_b,
+                 const int32_t* lengths, float* scores, int64_t B, int64_t Lq, int64_t Ld, int64_t d,
+                 void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_common(1, B, Lq, Ld, d, q_stride_l, d_stride_b, d_stride_l, 1);
+  if (rc) return rc;
+  if (B == 0) return ok();
+  if (!Q || !D || !scores || !scales || !mins)
+    return fail(FMX_ERR_INVALID, "Q, D, scales, mins and scores must be non-null");
+  if (!aligned16(Q) || !aligned16(D)) return fail(FMX_ERR_INVALID, "Q and D must be 16-byte aligned");
+  if ((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(mins)) & 1u)
+    return fail(FMX_ERR_INVALID, "scales and mins must be 2-byte aligned");
+  if (sm_stride_b < Ld) return fail(FMX_ERR_INVALID, "scale doc stride %lld < Ld", (long long)sm_stride_b);
+  const size_t need = fwd_ws_bytes(1, B, Lq, d);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(FMX_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+
+  fmx::FwdArgs a = {};
+  a.Q = Q;
+  a.D = D;
+  a.lengths = lengths;
+  a.scores = scores;
+  a.argmax = nullptr;
+  a.scales = static_cast<const uint16_t*>(scales);
+  a.mins = static_cast<const uint16_t*>(mins);
+  a.partial = static_cast<float*>(workspace);
+  a.sq_n = 0;
+  a.sq_l = q_stride_l;
+  a.sd_b = d_stride_b;
+  a.sd_l = d_stride_l;
+  a.ss_n = 0;
+  a.ss_b = 1;
+  a.sm_b = sm_stride_b;
+  a.Nq = 1;
+  a.B = (int)B;
+  a.Lq = (int)Lq;
+  a.Lq_rows = (int)Lq;
+  a.Ld = (int)Ld;
+  a.d = (int)d;
+  a.shared_docs = 1;
+  // Four scales per 8-byte load needs 8-byte aligned doc rows of scales and a
+  // padded length that never passes the end of a doc's row.
+  a.sm_vec = ((sm_stride_b & 3) == 0 && (Ld & 3) == 0 &&
+              ((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(mins)) & 7u) == 0)
+                 ? 1
+                 : 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const hipError_t e = plan_fwd(Lq, d).splitd ? fmx::launch_splitd_fwd(fmx::KIND_U8, a, false, s)
+                                              : fmx::launch_stream_fwd(fmx::KIND_U8, a, false, s);
+  return hip_status(e, "fmx_fwd_int8 launch");
+}
+
+size_t fmx_fwd_sparse_workspace_bytes(int64_t B, int64_t K, int64_t Ld, int64_t d) {
+  (void)Ld;
+  return fwd_ws_bytes(1, B, K, d);
+}
+
+int fmx_fwd_sparse(int dtype, const void* Q, int64_t q_stride_l, int64_t Lq, const void* D,
+                   int64_t d_stride_b, int64_t d_stride_l, const int32_t* indices, int64_t idx_stride_b,
+                   int64_t idx_stride_k, int64_t K, const int32_t* lengths, float* scores, int64_t B,
+                   int64_t Ld, int64_t d, void* workspace, size_t workspace_bytes, void* stream) {
+  if (dtype != FMX_DTYPE_F16 && dtype != FMX_DTYPE_BF16) return fail(FMX_ERR_INVALID, "unknown dtype %d", dtype);
+  if (Lq < 1) return fail(FMX_ERR_INVALID, "Lq=%lld must be >= 1", (long long)Lq);
+  int rc = check_common(1, B, K > Lq ? K : Lq, Ld, d, q_stride_l, d_stride_b, d_stride_l, 2);
+  if (rc) return rc;
+  if (K < 1) return fail(FMX_ERR_INVALID, "K=%lld must be >= 1", (long long)K);
+  if (B == 0) return ok();
+  if (!Q || !D || !scores || !indices) return fail(FMX_ERR_INVALID, "Q, D, indices and scores must be non-null");
+  if (!aligned16(Q) || !aligned16(D)) return fail(FMX_ERR_INVALID, "Q and D must be 16-byte aligned");
+  const size_t need = fwd_ws_bytes(1, B, K, d);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(FMX_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+
+  fmx::FwdArgs a = {};
+  a.Q = Q;
+  a.D = D;
+  a.lengths = lengths;
+  a.scores = scores;
+  a.argmax = nullptr;
+  a.partial = static_cast<float*>(workspace);
+  a.qidx = indices;
+  a.si_b = idx_stride_b;
+  a.si_k = idx_stride_k;
+  a.sq_n = 0;
+  a.sq_l = q_stride_l;
+  a.sd_b = d_stride_b;
+  a.sd_l = d_stride_l;
+  a.ss_n = 0;
+  a.ss_b = 1;
+  a.Nq = 1;
+  a.B = (int)B;
+  a.Lq = (int)K;
+  a.Lq_rows = (int)Lq;
+  a.Ld = (int)Ld;
+  a.d = (int)d;
+  a.shared_docs = 1;
+  const int kind = dtype == FMX_DTYPE_BF16 ? fmx::KIND_BF16 : fmx::KIND_F16;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const hipError_t e = plan_fwd(K, d).splitd ? fmx::launch_splitd_fwd(kind, a, false, s)
+                                             : fmx::launch_stream_fwd(kind, a, false, s);
+  return hip_status(e, "fmx_fwd_sparse launch");
+}
+
+size_t fmx_bwd_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld, int64_t d) {
+  (void)Ld;
+  if (B < 0 || Lq < 1 || d < 1) return 0;
+  return (size_t)fmx::bwd_dq_chunks((int)B, (int)Lq, (int)d) * (size_t)Lq * (size_t)d * sizeof(float);
+}
+
+int fmx_bwd(int dtype, const void* Q, int64_t q_stride_l, const void* D, int64_t d_stride_b,
+            int64_t d_stride_l, const int32_t* argmax, const float* grad_scores, void* dQ, void* dD,
+            int64_t B, int64_t Lq, int64_t Ld, int64_t d, void* workspace, size_t workspace_bytes,
+            void* stream) {
+  if (dtype != FMX_DTYPE_F16 && dtype != FMX_DTYPE_BF16) return fail(FMX_ERR_INVALID, "unknown dtype %d", dtype);
+  int rc = check_common(1, B, Lq, Ld, d, q_stride_l, d_stride_b, d_stride_l, 2);
+  if (rc) return rc;
+  if (Ld < 1) return fail(FMX_ERR_INVALID, "backward needs Ld >= 1");
+  if (!dQ && !dD) return ok();
+  if (!Q || !D || !argmax || !grad_scores) return fail(FMX_ERR_INVALID, "Q, D, argmax and grad must be non-null");
+  if (!aligned16(Q) || !aligned16(D)) return fail(FMX_ERR_INVALID, "Q and D must be 16-byte aligned");
+  if ((dQ && !aligned16(dQ)) || (dD && !aligned16(dD))) return fail(FMX_ERR_INVALID, "dQ and dD must be 16-byte aligned");
+  if (fmx::bwd_dd_lds_bytes((int)Lq, (int)Ld) > 64 * 1024)
+    return fail(FMX_ERR_UNSUPPORTED, "Lq=%lld, Ld=%lld exceed the dD kernel's LDS", (long long)Lq, (long long)Ld);
+  const size_t need = fmx_bwd_workspace_bytes(B, Lq, Ld, d);
+  if (dQ && (!workspace || workspace_bytes < need))
+    return fail(FMX_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+
+  fmx::BwdArgs a = {};
+  a.Q = Q;
+  a.D = D;
+  a.argmax = argmax;
+  a.grad = grad_scores;
+  a.dQ = dQ;
+  a.dD = dD;
+  a.ws = static_cast<float*>(workspace);
+  a.sq_l = q_stride_l;
+  a.sd_b = d_stride_b;
+  a.sd_l = d_stride_l;
+  a.B = (int)B;
+  a.Lq = (int)Lq;
+  a.Ld = (int)Ld;
+  a.d = (int)d;
+  a.nchunk = fmx::bwd_dq_chunks((int)B, (int)Lq, (int)d);
+  const int kind = dtype == FMX_DTYPE_BF16 ? fmx::KIND_BF16 : fmx::KIND_F16;
+  return hip_status(fmx::launch_bwd(kind, a, static_cast<hipStream_t>(stream)), "fmx_bwd launch");
+}
+
+}  // extern "C"

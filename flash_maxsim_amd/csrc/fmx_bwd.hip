@@ -1,0 +1,214 @@
+// Argmax backward of single-query MaxSim.
+//
+// Replaces _maxsim_bwd_dQ_kernel and _maxsim_bwd_dD_kernel (reference
+// flash_maxsim/flash_maxsim.py:153-188) with the same mathematics:
+//   dQ[q, :]    = sum_b g[b] * D[b, a[b, q], :]
+//   dD[b, j, :] = g[b] * sum_{q : a[b, q] = j} Q[q, :]
+// Differences by design:
+//  * dQ is a two-stage gather-reduce: doc chunks accumulate fp32 partials in a
+//    caller workspace, then a second kernel adds the chunks in order. The
+//    reference runs one program per query token looping over every doc.
+//  * dD is written exactly once per element by the doc's workgroup (zeros for
+//    rows no query token picked, the fp32 sum for picked rows), so there is no
+//    torch.zeros_like memset and no fp16 atomics; results are bitwise
+//    deterministic.
+#include "fmx_device.h"
+#include "fmx_kernels.h"
+
+namespace fmx {
+namespace {
+
+template <bool BF>
+struct Elem;
+template <>
+struct Elem<false> {
+  static __device__ __forceinline__ float to_f(uint16_t v) { return (float)__builtin_bit_cast(_Float16, v); }
+  static __device__ __forceinline__ uint16_t from_f(float x) {
+    return __builtin_bit_cast(uint16_t, (_Float16)x);
+  }
+};
+template <>
+struct Elem<true> {
+  static __device__ __forceinline__ float to_f(uint16_t v) {
+    return __builtin_bit_cast(float, (uint32_t)v << 16);
+  }
+  static __device__ __forceinline__ uint16_t from_f(float x) {
+    return __builtin_bit_cast(uint16_t, (__bf16)x);
+  }
+};
+
+// Loads elements k0 .. k0+7 (those < d) of a 2-byte row as fp32.
+template <bool BF>
+__device__ __forceinline__ void load8(const uint16_t* row, int k0, int d, float (&x)[8]) {
+  if (k0 + 8 <= d) {
+    const uint4 v = *reinterpret_cast<const uint4*>(row + k0);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = Elem<BF>::to_f(w[e] & 0xffffu);
+      x[2 * e + 1] = Elem<BF>::to_f(w[e] >> 16);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = (k0 + e < d) ? Elem<BF>::to_f(row[k0 + e]) : 0.f;
+  }
+}
+
+// Stores elements k0 .. k0+7 (those < d); 16-byte stores need d % 8 == 0 so
+// that every row of the contiguous output starts 16-byte aligned.
+template <bool BF>
+__device__ __forceinline__ void store8(uint16_t* row, int k0, int d, const float (&x)[8]) {
+  if ((d & 7) == 0) {
+    uint4 v;
+    v.x = (uint32_t)Elem<BF>::from_f(x[0]) | ((uint32_t)Elem<BF>::from_f(x[1]) << 16);
+    v.y = (uint32_t)Elem<BF>::from_f(x[2]) | ((uint32_t)Elem<BF>::from_f(x[3]) << 16);
+    v.z = (uint32_t)Elem<BF>::from_f(x[4]) | ((uint32_t)Elem<BF>::from_f(x[5]) << 16);
+    v.w = (uint32_t)Elem<BF>::from_f(x[6]) | ((uint32_t)Elem<BF>::from_f(x[7]) << 16);
+    *reinterpret_cast<uint4*>(row + k0) = v;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (k0 + e < d) row[k0 + e] = Elem<BF>::from_f(x[e]);
+  }
+}
+
+__device__ __forceinline__ int clamp_index(int j, int Ld) { return j < 0 ? 0 : (j >= Ld ? Ld - 1 : j); }
+
+// Stage 1 of dQ: one thread per (query token q, 8-wide k chunk), one grid row
+// per chunk of docs; ws[chunk][q][k] = sum over the chunk's docs, in order.
+template <bool BF>
+__global__ void __launch_bounds__(256) bwd_dq_partial_kernel(BwdArgs a) {
+  const int nkc = (a.d + 7) >> 3;
+  const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (tid >= (int64_t)a.Lq * nkc) return;
+  const int q = (int)(tid / nkc);
+  const int k0 = (int)(tid - (int64_t)q * nkc) * 8;
+  const int per = (a.B + a.nchunk - 1) / a.nchunk;
+  const int b0 = blockIdx.y * per;
+  const int b1 = min(a.B, b0 + per);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const uint16_t* D = static_cast<const uint16_t*>(a.D);
+#pragma unroll 4
+  for (int b = b0; b < b1; ++b) {
+    const int j = clamp_index(a.argmax[(int64_t)b * a.Lq + q], a.Ld);
+    const float gb = a.grad[b];
+    float x[8];
+    load8<BF>(D + (int64_t)b * a.sd_b + (int64_t)j * a.sd_l, k0, a.d, x);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = fmaf(gb, x[e], acc[e]);
+  }
+  float* out = a.ws + ((int64_t)blockIdx.y * a.Lq + q) * a.d + k0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (k0 + e < a.d) out[e] = acc[e];
+}
+
+// Stage 2 of dQ: dQ[q][k] = sum over chunks (in order) of ws[chunk][q][k].
+template <bool BF>
+__global__ void __launch_bounds__(256) bwd_dq_finalize_kernel(BwdArgs a) {
+  const int64_t n = (int64_t)a.Lq * a.d;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  float s = 0.f;
+  for (int c = 0; c < a.nchunk; ++c) s += a.ws[(int64_t)c * n + i];
+  static_cast<uint16_t*>(a.dQ)[i] = Elem<BF>::from_f(s);
+}
+
+// dD for one doc per workgroup. LDS: argmax row, query tokens sorted by
+// (row, token), and a bitmap of rows picked by some token.
+template <bool BF>
+__global__ void __launch_bounds__(256) bwd_dd_kernel(BwdArgs a) {
+  extern __shared__ int smem[];
+  int* am = smem;
+  int* order = smem + a.Lq;
+  uint32_t* hit = reinterpret_cast<uint32_t*>(smem + 2 * a.Lq);
+  const int b = blockIdx.x;
+  const int nwords = (a.Ld + 31) >> 5;
+  for (int i = threadIdx.x; i < nwords; i += 256) hit[i] = 0u;
+  for (int q = threadIdx.x; q < a.Lq; q += 256) am[q] = clamp_index(a.argmax[(int64_t)b * a.Lq + q], a.Ld);
+  __syncthreads();
+  for (int q = threadIdx.x; q < a.Lq; q += 256) {
+    const int j = am[q];
+    atomicOr(&hit[j >> 5], 1u << (j & 31));
+    int rank = 0;
+    for (int q2 = 0; q2 < a.Lq; ++q2) {
+      const int j2 = am[q2];
+      rank += (j2 < j) || (j2 == j && q2 < q);
+    }
+    order[rank] = q;
+  }
+  __syncthreads();
+
+  const float gb = a.grad[b];
+  const int nkc = (a.d + 7) >> 3;
+  uint16_t* out = static_cast<uint16_t*>(a.dD) + (int64_t)b * a.Ld * a.d;
+  const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const int64_t zn = (int64_t)a.Ld * nkc;
+  for (int64_t e = threadIdx.x; e < zn; e += 256) {
+    const int row = (int)(e / nkc);
+    const int k0 = (int)(e - (int64_t)row * nkc) * 8;
+    if (!((hit[row >> 5] >> (row & 31)) & 1u)) store8<BF>(out + (int64_t)row * a.d, k0, a.d, zero);
+  }
+  const uint16_t* Q = static_cast<const uint16_t*>(a.Q);
+  const int64_t hn = (int64_t)a.Lq * nkc;
+  for (int64_t e = threadIdx.x; e < hn; e += 256) {
+    const int p = (int)(e / nkc);
+    const int k0 = (int)(e - (int64_t)p * nkc) * 8;
+    const int j = am[order[p]];
+    if (p > 0 && am[order[p - 1]] == j) continue;  // not the first token of its row group
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int p2 = p; p2 < a.Lq && am[order[p2]] == j; ++p2) {
+      float x[8];
+      load8<BF>(Q + (int64_t)order[p2] * a.sq_l, k0, a.d, x);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) acc[k] += x[k];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc[k] *= gb;
+    store8<BF>(out + (int64_t)j * a.d, k0, a.d, acc);
+  }
+}
+
+template <bool BF>
+hipError_t launch_bwd_t(const BwdArgs& a, hipStream_t s) {
+  const int nkc = (a.d + 7) >> 3;
+  if (a.dQ) {
+    const int64_t threads = (int64_t)a.Lq * nkc;
+    hipLaunchKernelGGL(bwd_dq_partial_kernel<BF>, dim3((unsigned)((threads + 255) / 256), a.nchunk), dim3(256),
+                       0, s, a);
+    const int64_t n = (int64_t)a.Lq * a.d;
+    hipLaunchKernelGGL(bwd_dq_finalize_kernel<BF>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
+  }
+  if (a.dD && a.B > 0) {
+    const size_t lds = (size_t)(2 * a.Lq + (a.Ld + 31) / 32) * sizeof(int);
+    hipLaunchKernelGGL(bwd_dd_kernel<BF>, dim3((unsigned)a.B), dim3(256), lds, s, a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+// Doc chunks of the dQ gather: enough (q, k-chunk, doc-chunk) threads to keep
+// the GPU's loads in flight (about 2^19), at most 64 chunks, at least 8 docs each.
+int bwd_dq_chunks(int B, int Lq, int d) {
+  if (B <= 0) return 1;
+  const int64_t per_chunk = (int64_t)Lq * ((d + 7) / 8);
+  int64_t n = ((int64_t)1 << 19) / (per_chunk > 0 ? per_chunk : 1);
+  const int64_t by_docs = (B + 7) / 8;
+  if (n > by_docs) n = by_docs;
+  if (n > 64) n = 64;
+  if (n < 1) n = 1;
+  return (int)n;
+}
+
+size_t bwd_dd_lds_bytes(int Lq, int Ld) { return (size_t)(2 * Lq + (Ld + 31) / 32) * sizeof(int); }
+
+hipError_t launch_bwd(int kind, const BwdArgs& a, hipStream_t s) {
+  switch (kind) {
+    case KIND_F16: return launch_bwd_t<false>(a, s);
+    case KIND_BF16: return launch_bwd_t<true>(a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace fmx

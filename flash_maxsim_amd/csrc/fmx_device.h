@@ -1,0 +1,134 @@
+// Device-side building blocks shared by every flash_maxsim kernel on gfx950
+// (CDNA4, wave64): operand vector types, raw buffer resources, the fp16/bf16
+// MFMA wrapper, exact uint8 -> fp16 code conversion and wave reductions.
+//
+// Fragment convention used throughout (v_mfma_f32_16x16x32_{f16,bf16}):
+//   lane l = 16*g + c   (c = l % 16, g = l / 16)
+//   A operand (16 x 32, M x K): lane l holds row c, k = 8*g .. 8*g+7
+//   B operand (32 x 16, K x N): lane l holds col c, k = 8*g .. 8*g+7
+//   C/D       (16 x 16)       : lane l holds rows 4*g .. 4*g+3 of col c
+// A k-step t of a d-wide row therefore covers k = 32*t + 8*g .. +7 for lane l.
+// Any permutation of k applied identically to A and B leaves A*B unchanged, so
+// both operands are loaded with the same (row, 32*t + 8*g) addressing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fmx {
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// Element kinds of the document operand.
+enum Kind : int { KIND_F16 = 0, KIND_BF16 = 1, KIND_U8 = 2 };
+
+template <int KIND> struct KindInfo;
+template <> struct KindInfo<KIND_F16> { static constexpr int esz = 2; static constexpr bool bf = false; };
+template <> struct KindInfo<KIND_BF16> { static constexpr int esz = 2; static constexpr bool bf = true; };
+// uint8 codes are widened to fp16 and multiplied against an fp16 query.
+template <> struct KindInfo<KIND_U8> { static constexpr int esz = 1; static constexpr bool bf = false; };
+
+// Raw (unswizzled, stride 0) buffer resource. Word 3 = 0x00020000 selects the
+// 32-bit data format gfx9-family buffer instructions expect. A load whose byte
+// offset is >= num_records returns zeros without touching memory; the kernels
+// use that both for the doc-length tail and for k >= d.
+constexpr uint32_t kBufWord3 = 0x00020000u;
+constexpr uint32_t kOOB = 0x80000000u;  // kernels keep num_records < 2^31
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           (int)kBufWord3);
+}
+
+__device__ __forceinline__ u32x4_t ld16(rsrc_t r, uint32_t voff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
+}
+__device__ __forceinline__ u32x2_t ld8(rsrc_t r, uint32_t voff) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, voff, 0, 0);
+}
+__device__ __forceinline__ uint16_t ld2(rsrc_t r, uint32_t voff) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, voff, 0, 0);
+}
+
+// 16x16x32 MFMA, fp32 accumulate. Operands travel as raw 128-bit registers.
+template <bool BF>
+__device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
+  if constexpr (BF) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+}
+
+// Eight uint8 codes -> eight fp16 values equal to the codes, exactly.
+// v_perm places code byte c under exponent byte 0x64, giving the fp16 value
+// 1024 + c (exact: 1024 + c < 2048 has an 11-bit significand); one packed fp16
+// subtraction of 1024 then leaves c exactly.
+__device__ __forceinline__ u32x4_t codes_to_f16(u32x2_t raw) {
+  const uint32_t hi = 0x64646464u;
+  u32x4_t h;
+  h[0] = __builtin_amdgcn_perm(hi, raw[0], 0x04010400u);
+  h[1] = __builtin_amdgcn_perm(hi, raw[0], 0x04030402u);
+  h[2] = __builtin_amdgcn_perm(hi, raw[1], 0x04010400u);
+  h[3] = __builtin_amdgcn_perm(hi, raw[1], 0x04030402u);
+  f16x8_t v = __builtin_bit_cast(f16x8_t, h);
+  v = v - (f16x8_t)((_Float16)1024.0f);
+  return __builtin_bit_cast(u32x4_t, v);
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+__device__ __forceinline__ float bf16_bits_to_float(uint32_t bits16) {
+  return __builtin_bit_cast(float, bits16 << 16);
+}
+
+// Sum of the 8 fp16 / bf16 elements packed in a fragment, in fp32.
+template <bool BF>
+__device__ __forceinline__ float frag_sum(u32x4_t v) {
+  float s = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    if constexpr (BF) {
+      s += bf16_bits_to_float(v[w] & 0xffffu) + bf16_bits_to_float(v[w] >> 16);
+    } else {
+      s += half_bits_to_float(v[w] & 0xffffu) + half_bits_to_float(v[w] >> 16);
+    }
+  }
+  return s;
+}
+
+// Mask keeping the first n (0..8) 16-bit elements of an 8-element fragment.
+__device__ __forceinline__ u32x4_t prefix_mask16(int n) {
+  u32x4_t m;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    m[w] = (2 * w + 2 <= n) ? 0xffffffffu : ((2 * w + 1 <= n) ? 0x0000ffffu : 0u);
+  }
+  return m;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) v += __shfl_xor(v, s);
+  return v;
+}
+
+// (value, index) max where ties go to the smaller index: combining per-lane
+// first-occurrence maxima this way yields the global first occurrence.
+__device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
+  if (ov > v || (ov == v && oi < i)) {
+    v = ov;
+    i = oi;
+  }
+}
+
+}  // namespace fmx

@@ -1,0 +1,311 @@
+// Split-d MaxSim forward for large embeddings (256 < d <= 2048).
+//
+// Same contract as _maxsim_fwd_kernel / _maxsim_int8_kernel (reference
+// flash_maxsim/flash_maxsim.py:80-146, flash_maxsim/flash_maxsim_quant.py:40-98)
+// for shapes whose query tile does not fit one wave's registers. The reference
+// covers those with small Triton blocks (d_pad up to 2048, flash_maxsim.py:29-34).
+//
+// One workgroup of eight waves scores one (query, doc) pair for one pass of up
+// to 16*NQB query tokens. Wave w owns the k-steps [w*KSW, (w+1)*KSW), i.e. the
+// dims [32*KSW*w, 32*KSW*(w+1)): it holds that slice of the query tile in VGPRs
+// and streams the same slice of every 16-token doc tile straight from HBM.
+// Per tile each wave's MFMAs give a partial S over its slice; the partials
+// meet in LDS, where wave nb sums the eight slices of
+// query block nb in wave order (deterministic), applies the uint8 affine
+// epilogue and the length mask, and folds the rows into its running max. The
+// max therefore always sees the full-d similarity, never a partial one.
+#include "fmx_kernels.h"
+#include "fmx_tile.h"
+
+namespace fmx {
+namespace {
+
+constexpr int kSplitWaves = 8;
+
+template <int KIND, int NQB, int KSW, bool KMASK, bool ARGMAX>
+__global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
+  constexpr int NW = kSplitWaves, QROWS = NQB * 16;
+  constexpr int P = KSW >= 8 ? 2 : 3;  // tiles in flight per wave
+  constexpr int ESZ = KindInfo<KIND>::esz;
+  constexpr bool BF = KindInfo<KIND>::bf;
+  constexpr bool U8 = KIND == KIND_U8;
+  static_assert(NQB <= NW, "one owning wave per query block");
+  __shared__ f32x4_t part[NW][NQB][64];
+  __shared__ float qs_part[U8 ? NW : 1][QROWS];
+  __shared__ float red_m[QROWS];
+  __shared__ int red_i[ARGMAX ? QROWS : 1];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, g = lane >> 4;
+  const int pass = blockIdx.y;
+  int qi, b;
+  if (a.shared_docs && a.Nq > 1) {
+    b = blockIdx.x / a.Nq;
+    qi = blockIdx.x - b * a.Nq;
+  } else {
+    qi = blockIdx.x / a.B;
+    b = blockIdx.x - qi * a.B;
+  }
+  const int item = qi * a.B + b;
+  const int64_t drow = a.shared_docs ? (int64_t)b : (int64_t)item;
+  int len = a.lengths ? a.lengths[drow] : a.Ld;
+  len = len < 0 ? 0 : (len > a.Ld ? a.Ld : len);
+  const int ntiles = (len + 15) >> 4;
+  const bool owner = wave < NQB;  // wave w reduces and maxes query block w
+
+  const int tbase = wave * KSW;  // first global k-step of this wave
+  const int kp = a.d & ~7;
+  const int tp = (kp >> 5) - tbase;  // local k-step of the partial group, if any
+  const u32x4_t pmask = prefix_mask16(g == ((kp >> 3) & 3) ? (a.d & 7) : 8);
+  const bool has_partial = KMASK && (a.d & 7) != 0;
+
+  // ---- query slice of this pass ----
+  const int q0 = pass * QROWS;
+  const rsrc_t rq = make_rsrc((const char*)a.Q + (int64_t)qi * a.sq_n * 2, (uint32_t)(a.Lq_rows * a.sq_l * 2));
+  u32x4_t qf[NQB][KSW];
+#pragma unroll
+  for (int nb = 0; nb < NQB; ++nb) {
+    const uint32_t rowoff = query_row_offset(a, b, q0 + nb * 16 + c);
+#pragma unroll
+    for (int t = 0; t < KSW; ++t) {
+      const int k0 = 32 * (tbase + t) + 8 * g;
+      if constexpr (KMASK) {
+        qf[nb][t] = ld16(rq, k0 < a.d ? rowoff + (uint32_t)(k0 * 2) : kOOB);
+        if (has_partial && t == tp) qf[nb][t] &= pmask;
+      } else {
+        qf[nb][t] = ld16(rq, rowoff + (uint32_t)(k0 * 2));
+      }
+    }
+  }
+  float qsum = 0.f;  // owner waves, uint8 docs: full-d sum of query token 16*wave + c
+  if constexpr (U8) {
+#pragma unroll
+    for (int nb = 0; nb < NQB; ++nb) {
+      float s = 0.f;
+#pragma unroll
+      for (int t = 0; t < KSW; ++t) s += frag_sum<false>(qf[nb][t]);
+      s += __shfl_xor(s, 16);
+      s += __shfl_xor(s, 32);
+      if (g == 0) qs_part[wave][nb * 16 + c] = s;
+    }
+    __syncthreads();
+    if (owner) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w) qsum += qs_part[w][wave * 16 + c];
+    }
+  }
+
+  // ---- doc stream ----
+  const DocRes dr = make_doc_res<KIND>(a.D, drow, a.sd_b, a.sd_l, len, a.scales, a.mins, a.sm_b, a.sm_vec);
+  uint32_t koff[KSW];
+#pragma unroll
+  for (int t = 0; t < KSW; ++t) {
+    const int k0 = 32 * (tbase + t) + 8 * g;
+    koff[t] = (KMASK && k0 >= a.d) ? kOOB : (uint32_t)(k0 * ESZ);  // past d: zeros
+  }
+
+  float m = -INFINITY;
+  int mi = 0;
+  Tile<KIND, KSW> buf[P];
+#pragma unroll
+  for (int s = 0; s < P; ++s)
+    if (s < ntiles) load_tile<KIND, KSW>(buf[s], dr, s, c, g, koff);
+  for (int i0 = 0; i0 < ntiles; i0 += P) {
+#pragma unroll
+    for (int s = 0; s < P; ++s) {
+      const int tile = i0 + s;
+      if (tile < ntiles) {
+        u32x4_t af[KSW];
+#pragma unroll
+        for (int t = 0; t < KSW; ++t) {
+          af[t] = tile_operand<KIND, KSW>(buf[s], t);
+          if constexpr (KMASK && !U8) {
+            if (has_partial && t == tp) af[t] &= pmask;
+          }
+        }
+        float sc[4], mn[4];
+        if constexpr (U8) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            sc[r] = tile_scale(buf[s].s, r);
+            mn[r] = tile_scale(buf[s].m, r);
+          }
+        }
+        if (tile + P < ntiles) load_tile<KIND, KSW>(buf[s], dr, tile + P, c, g, koff);
+
+#pragma unroll
+        for (int nb = 0; nb < NQB; ++nb) {
+          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int t = 0; t < KSW; ++t) acc = mfma16x16x32<BF>(af[t], qf[nb][t], acc);
+          part[wave][nb][lane] = acc;
+        }
+        __syncthreads();
+        if (owner) {
+          f32x4_t S = part[0][wave][lane];
+#pragma unroll
+          for (int w = 1; w < NW; ++w) S += part[w][wave][lane];
+          if constexpr (U8) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) S[r] = fmaf(sc[r], S[r], mn[r] * qsum);
+          }
+          const int row0 = tile * 16 + 4 * g;
+          if (tile * 16 + 16 > len) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (row0 + r >= len) S[r] = -INFINITY;
+          }
+          if constexpr (ARGMAX) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              if (S[r] > m) {
+                m = S[r];
+                mi = row0 + r;
+              }
+            }
+          } else {
+            m = fmaxf(m, fmaxf(fmaxf(S[0], S[1]), fmaxf(S[2], S[3])));
+          }
+        }
+        __syncthreads();
+      }
+    }
+  }
+
+  // ---- per query token: merge row groups, then sum the pass ----
+  if (owner) {
+    float v = m;
+    int ix = mi;
+#pragma unroll
+    for (int s = 16; s <= 32; s <<= 1) {
+      const float ov = __shfl_xor(v, s);
+      if constexpr (ARGMAX) {
+        const int oi = __shfl_xor(ix, s);
+        argmax_merge(v, ix, ov, oi);
+      } else {
+        v = fmaxf(v, ov);
+      }
+    }
+    if (g == 0) {
+      red_m[wave * 16 + c] = v;
+      if constexpr (ARGMAX) red_i[wave * 16 + c] = ix;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float partsum = 0.f;
+    for (int r = lane; r < QROWS; r += 64) {
+      const int q = q0 + r;
+      if (q < a.Lq) {
+        partsum += red_m[r];
+        if constexpr (ARGMAX) a.argmax[(int64_t)item * a.Lq + q] = red_i[r];
+      }
+    }
+    const float total = wave_sum(partsum);
+    if (lane == 0) {
+      if (gridDim.y == 1) {
+        a.scores[(int64_t)qi * a.ss_n + (int64_t)b * a.ss_b] = total;
+      } else {
+        a.partial[(int64_t)pass * gridDim.x + item] = total;  // gridDim.x == Nq*B
+      }
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256) splitd_sum_passes_kernel(FwdArgs a, int npass) {
+  const int64_t items = (int64_t)a.Nq * a.B;
+  const int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= items) return;
+  float s = 0.f;
+  for (int p = 0; p < npass; ++p) s += a.partial[(int64_t)p * items + item];
+  const int64_t qi = item / a.B, b = item - qi * a.B;
+  a.scores[qi * a.ss_n + b * a.ss_b] = s;
+}
+
+template <int KIND, int NQB, int KSW, bool KMASK, bool ARGMAX>
+hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
+  constexpr int QROWS = NQB * 16;
+  const int npass = (a.Lq + QROWS - 1) / QROWS;
+  const int64_t items = (int64_t)a.Nq * a.B;
+  hipLaunchKernelGGL((splitd_fwd_kernel<KIND, NQB, KSW, KMASK, ARGMAX>), dim3((unsigned)items, npass),
+                     dim3(512), 0, s, a);
+  if (npass > 1) {
+    hipLaunchKernelGGL(splitd_sum_passes_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, a,
+                       npass);
+  }
+  return hipGetLastError();
+}
+
+template <int KIND, int NQB, int KSW>
+hipError_t dispatch_flags(const FwdArgs& a, bool am, hipStream_t s) {
+  const bool kmask = a.d != 32 * KSW * kSplitWaves;
+  if constexpr (KIND == KIND_U8) {
+    (void)am;
+    return kmask ? launch_one<KIND, NQB, KSW, true, false>(a, s) : launch_one<KIND, NQB, KSW, false, false>(a, s);
+  } else {
+    if (kmask) return am ? launch_one<KIND, NQB, KSW, true, true>(a, s) : launch_one<KIND, NQB, KSW, true, false>(a, s);
+    return am ? launch_one<KIND, NQB, KSW, false, true>(a, s) : launch_one<KIND, NQB, KSW, false, false>(a, s);
+  }
+}
+
+template <int KIND, int KSW>
+hipError_t dispatch_nqb(const FwdArgs& a, bool am, hipStream_t s) {
+  switch (splitd_fwd_nqb(a.Lq, a.d)) {
+    case 1: return dispatch_flags<KIND, 1, KSW>(a, am, s);
+    case 2: return dispatch_flags<KIND, 2, KSW>(a, am, s);
+    case 4:
+      if constexpr (KSW <= 4) return dispatch_flags<KIND, 4, KSW>(a, am, s);
+      return hipErrorInvalidValue;
+    default:
+      if constexpr (KSW <= 4) return dispatch_flags<KIND, 8, KSW>(a, am, s);
+      return hipErrorInvalidValue;
+  }
+}
+
+template <int KIND>
+hipError_t dispatch_ksw(const FwdArgs& a, bool am, hipStream_t s) {
+  switch (splitd_fwd_ksw(a.d)) {
+    case 2: return dispatch_nqb<KIND, 2>(a, am, s);
+    case 4: return dispatch_nqb<KIND, 4>(a, am, s);
+    case 8: return dispatch_nqb<KIND, 8>(a, am, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+bool splitd_fwd_supported(int d) { return d > 256 && d <= 2048; }
+
+// k-steps per wave: the eight slices of 32*KSW cover d.
+int splitd_fwd_ksw(int d) {
+  const int steps = (d + 31) / 32;
+  const int ksw = (steps + kSplitWaves - 1) / kSplitWaves;
+  return ksw <= 2 ? 2 : ksw <= 4 ? 4 : 8;
+}
+
+// Query blocks per pass, capped so the query slice stays within 128 VGPRs
+// (64 at KSW = 8, where the deeper doc fragments need the rest).
+int splitd_fwd_nqb(int Lq, int d) {
+  const int need = (Lq + 15) / 16;
+  const int ksw = splitd_fwd_ksw(d);
+  const int cap = ksw >= 8 ? 2 : 32 / ksw;
+  const int nqb = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
+  return nqb < cap ? nqb : cap;
+}
+
+int splitd_fwd_passes(int Lq, int d) {
+  const int rows = 16 * splitd_fwd_nqb(Lq, d);
+  return (Lq + rows - 1) / rows;
+}
+
+hipError_t launch_splitd_fwd(int kind, const FwdArgs& a, bool with_argmax, hipStream_t s) {
+  switch (kind) {
+    case KIND_F16: return dispatch_ksw<KIND_F16>(a, with_argmax, s);
+    case KIND_BF16: return dispatch_ksw<KIND_BF16>(a, with_argmax, s);
+    case KIND_U8: return dispatch_ksw<KIND_U8>(a, false, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace fmx

@@ -1,0 +1,321 @@
+// Streaming MaxSim forward for d <= 256 (the HBM-bound small-query regime).
+//
+// Replaces the per-(query, doc) Triton program of _maxsim_fwd_kernel
+// (reference flash_maxsim/flash_maxsim.py:80-146) and _maxsim_int8_kernel
+// (flash_maxsim/flash_maxsim_quant.py:40-98).
+//
+// One workgroup of four waves scores one (query, doc) pair for one pass of up
+// to 16*NQB query tokens:
+//  * the pass's query tile (16*NQB tokens x 32*KS dims) sits in VGPRs as MFMA
+//    B-fragments for the whole doc;
+//  * the doc's 16-token tiles are dealt round-robin to the four waves, which
+//    load them with 128-bit (fp16/bf16) or 64-bit (uint8) buffer loads straight
+//    into VGPRs, P tiles deep, so no LDS round trip sits on the HBM stream;
+//  * S = D_tile * Q^T runs on v_mfma_f32_16x16x32 with fp32 accumulation and
+//    each lane folds its 4 result rows into a running per-query-token max
+//    (plus the first index reaching it, when argmax is requested);
+//  * at the end lanes merge across row groups with cross-lane shuffles, waves
+//    merge through LDS, and wave 0 sums over query tokens into one fp32 score.
+// uint8 docs use S = scale_j * (Q . codes_j) + min_j * sum_k Q_k with the
+// codes widened to fp16 exactly, which equals Q . dequantize(codes) in fp32.
+// Queries longer than 16*NQB tokens run as blockIdx.y passes whose partial sums
+// a second kernel adds in pass order.
+#include "fmx_kernels.h"
+#include "fmx_tile.h"
+
+namespace fmx {
+namespace {
+
+constexpr int kStreamWaves = 4;
+constexpr int kStreamDepth = 4;  // tiles in flight per wave
+
+// KMASK: d is not exactly 32*KS, so fragment slots past d must read as zero.
+template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX>
+__global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
+  constexpr int NW = kStreamWaves, P = kStreamDepth, QROWS = NQB * 16;
+  constexpr int ESZ = KindInfo<KIND>::esz;
+  constexpr bool BF = KindInfo<KIND>::bf;
+  constexpr bool U8 = KIND == KIND_U8;
+  __shared__ float red_m[NW][QROWS];
+  __shared__ int red_i[ARGMAX ? NW : 1][QROWS];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, g = lane >> 4;
+  const int pass = blockIdx.y;
+  int qi, b;
+  if (a.shared_docs && a.Nq > 1) {
+    // Queries of one doc run back to back so the doc streams from HBM once
+    // and the other queries find it in cache.
+    b = blockIdx.x / a.Nq;
+    qi = blockIdx.x - b * a.Nq;
+  } else {
+    qi = blockIdx.x / a.B;
+    b = blockIdx.x - qi * a.B;
+  }
+  const int item = qi * a.B + b;  // row of argmax / partial, as in the reference
+  const int64_t drow = a.shared_docs ? (int64_t)b : (int64_t)item;
+  int len = a.lengths ? a.lengths[drow] : a.Ld;
+  len = len < 0 ? 0 : (len > a.Ld ? a.Ld : len);
+  const int ntiles = (len + 15) >> 4;
+  const int my_n = ntiles > wave ? (ntiles - wave + NW - 1) / NW : 0;
+
+  // Partial 8-wide group (d % 8 != 0): fragment slot tp of lane group gp.
+  const int kp = a.d & ~7;
+  const int tp = kp >> 5;
+  const u32x4_t pmask = prefix_mask16(g == ((kp >> 3) & 3) ? (a.d & 7) : 8);
+  const bool has_partial = KMASK && (a.d & 7) != 0;
+
+  // ---- query tile of this pass (B operand) ----
+  const int q0 = pass * QROWS;
+  const rsrc_t rq = make_rsrc((const char*)a.Q + (int64_t)qi * a.sq_n * 2, (uint32_t)(a.Lq_rows * a.sq_l * 2));
+  u32x4_t qf[NQB][KS];
+  float qsum[NQB];
+#pragma unroll
+  for (int nb = 0; nb < NQB; ++nb) {
+    const uint32_t rowoff = query_row_offset(a, b, q0 + nb * 16 + c);
+#pragma unroll
+    for (int t = 0; t < KS; ++t) {
+      const int k0 = 32 * t + 8 * g;
+      if constexpr (KMASK) {
+        qf[nb][t] = ld16(rq, k0 < a.d ? rowoff + (uint32_t)(k0 * 2) : kOOB);
+        if (has_partial && t == tp) qf[nb][t] &= pmask;
+      } else {
+        qf[nb][t] = ld16(rq, rowoff + (uint32_t)(k0 * 2));
+      }
+    }
+    qsum[nb] = 0.f;
+    if constexpr (U8) {
+      float s = 0.f;
+#pragma unroll
+      for (int t = 0; t < KS; ++t) s += frag_sum<false>(qf[nb][t]);
+      s += __shfl_xor(s, 16);
+      s += __shfl_xor(s, 32);
+      qsum[nb] = s;
+    }
+  }
+
+  // ---- doc stream ----
+  const DocRes dr = make_doc_res<KIND>(a.D, drow, a.sd_b, a.sd_l, len, a.scales, a.mins, a.sm_b, a.sm_vec);
+  uint32_t koff[KS];
+#pragma unroll
+  for (int t = 0; t < KS; ++t) {
+    const int k0 = 32 * t + 8 * g;
+    // Slots past d read as zeros instead of touching the next row.
+    koff[t] = (KMASK && k0 >= a.d) ? kOOB : (uint32_t)(k0 * ESZ);
+  }
+
+  float m[NQB];
+  int mi[NQB];
+#pragma unroll
+  for (int nb = 0; nb < NQB; ++nb) {
+    m[nb] = -INFINITY;
+    mi[nb] = 0;
+  }
+
+  Tile<KIND, KS> buf[P];
+#pragma unroll
+  for (int s = 0; s < P; ++s)
+    if (s < my_n) load_tile<KIND, KS>(buf[s], dr, wave + NW * s, c, g, koff);
+  for (int i0 = 0; i0 < my_n; i0 += P) {
+#pragma unroll
+    for (int s = 0; s < P; ++s) {
+      const int i = i0 + s;
+      if (i < my_n) {
+        const int tile = wave + NW * i;
+        u32x4_t af[KS];
+#pragma unroll
+        for (int t = 0; t < KS; ++t) {
+          af[t] = tile_operand<KIND, KS>(buf[s], t);
+          if constexpr (KMASK && !U8) {
+            if (has_partial && t == tp) af[t] &= pmask;
+          }
+        }
+        float sc[4], mn[4];
+        if constexpr (U8) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            sc[r] = tile_scale(buf[s].s, r);
+            mn[r] = tile_scale(buf[s].m, r);
+          }
+        }
+        // The registers of slot s are free once converted: refill them now so
+        // the load overlaps this tile's MFMAs.
+        if (i + P < my_n) load_tile<KIND, KS>(buf[s], dr, wave + NW * (i + P), c, g, koff);
+
+        const int row0 = tile * 16 + 4 * g;
+        const bool tail = tile * 16 + 16 > len;
+#pragma unroll
+        for (int nb = 0; nb < NQB; ++nb) {
+          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int t = 0; t < KS; ++t) acc = mfma16x16x32<BF>(af[t], qf[nb][t], acc);
+          if constexpr (U8) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] = fmaf(sc[r], acc[r], mn[r] * qsum[nb]);
+          }
+          if (tail) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (row0 + r >= len) acc[r] = -INFINITY;
+          }
+          if constexpr (ARGMAX) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              if (acc[r] > m[nb]) {
+                m[nb] = acc[r];
+                mi[nb] = row0 + r;
+              }
+            }
+          } else {
+            m[nb] = fmaxf(m[nb], fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3])));
+          }
+        }
+      }
+    }
+  }
+
+  // ---- merge the four row groups of each query token, then the four waves ----
+#pragma unroll
+  for (int nb = 0; nb < NQB; ++nb) {
+    float v = m[nb];
+    int ix = mi[nb];
+#pragma unroll
+    for (int s = 16; s <= 32; s <<= 1) {
+      const float ov = __shfl_xor(v, s);
+      if constexpr (ARGMAX) {
+        const int oi = __shfl_xor(ix, s);
+        argmax_merge(v, ix, ov, oi);
+      } else {
+        v = fmaxf(v, ov);
+      }
+    }
+    if (g == 0) {
+      red_m[wave][nb * 16 + c] = v;
+      if constexpr (ARGMAX) red_i[wave][nb * 16 + c] = ix;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float part = 0.f;
+    for (int r = lane; r < QROWS; r += 64) {
+      float v = red_m[0][r];
+      int ix = ARGMAX ? red_i[0][r] : 0;
+#pragma unroll
+      for (int w = 1; w < NW; ++w) {
+        if constexpr (ARGMAX) {
+          argmax_merge(v, ix, red_m[w][r], red_i[w][r]);
+        } else {
+          v = fmaxf(v, red_m[w][r]);
+        }
+      }
+      const int q = q0 + r;
+      if (q < a.Lq) {
+        part += v;
+        if constexpr (ARGMAX) a.argmax[(int64_t)item * a.Lq + q] = ix;
+      }
+    }
+    const float total = wave_sum(part);
+    if (lane == 0) {
+      if (gridDim.y == 1) {
+        a.scores[(int64_t)qi * a.ss_n + (int64_t)b * a.ss_b] = total;
+      } else {
+        a.partial[(int64_t)pass * gridDim.x + item] = total;  // gridDim.x == Nq*B
+      }
+    }
+  }
+}
+
+// scores[qi, b] = sum over passes p (in order) of partial[p][qi*B + b].
+__global__ void __launch_bounds__(256) sum_passes_kernel(FwdArgs a, int npass) {
+  const int64_t items = (int64_t)a.Nq * a.B;
+  const int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= items) return;
+  float s = 0.f;
+  for (int p = 0; p < npass; ++p) s += a.partial[(int64_t)p * items + item];
+  const int64_t qi = item / a.B, b = item - qi * a.B;
+  a.scores[qi * a.ss_n + b * a.ss_b] = s;
+}
+
+template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX>
+hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
+  constexpr int QROWS = NQB * 16;
+  const int npass = (a.Lq + QROWS - 1) / QROWS;
+  const int64_t items = (int64_t)a.Nq * a.B;
+  hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX>), dim3((unsigned)items, npass),
+                     dim3(256), 0, s, a);
+  if (npass > 1) {
+    hipLaunchKernelGGL(sum_passes_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, a, npass);
+  }
+  return hipGetLastError();
+}
+
+template <int KIND, int NQB, int KS>
+hipError_t dispatch_flags(const FwdArgs& a, bool am, hipStream_t s) {
+  if constexpr (KIND == KIND_U8) {
+    (void)am;
+    return launch_one<KIND, NQB, KS, true, false>(a, s);
+  } else {
+    const bool kmask = a.d != 32 * KS;
+    if (kmask) return am ? launch_one<KIND, NQB, KS, true, true>(a, s) : launch_one<KIND, NQB, KS, true, false>(a, s);
+    return am ? launch_one<KIND, NQB, KS, false, true>(a, s) : launch_one<KIND, NQB, KS, false, false>(a, s);
+  }
+}
+
+template <int KIND, int KS>
+hipError_t dispatch_nqb(const FwdArgs& a, bool am, hipStream_t s) {
+  const int nqb = stream_fwd_nqb(a.Lq, a.d);
+  switch (nqb) {
+    case 1: return dispatch_flags<KIND, 1, KS>(a, am, s);
+    case 2: return dispatch_flags<KIND, 2, KS>(a, am, s);
+    case 4: return dispatch_flags<KIND, 4, KS>(a, am, s);
+    default:
+      if constexpr (KS <= 4) return dispatch_flags<KIND, 8, KS>(a, am, s);
+      return hipErrorInvalidValue;
+  }
+}
+
+template <int KIND>
+hipError_t dispatch_ks(const FwdArgs& a, bool am, hipStream_t s) {
+  switch (stream_fwd_ks(a.d)) {
+    case 1: return dispatch_nqb<KIND, 1>(a, am, s);
+    case 2: return dispatch_nqb<KIND, 2>(a, am, s);
+    case 4: return dispatch_nqb<KIND, 4>(a, am, s);
+    case 8: return dispatch_nqb<KIND, 8>(a, am, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+bool stream_fwd_supported(int d) { return d >= 1 && d <= 256; }
+
+int stream_fwd_ks(int d) {
+  const int ks = (d + 31) / 32;
+  return ks <= 1 ? 1 : ks <= 2 ? 2 : ks <= 4 ? 4 : 8;
+}
+
+// Query tokens per pass: as many 16-token blocks as Lq needs, capped so the
+// query tile stays within 128 VGPRs (NQB * KS <= 32).
+int stream_fwd_nqb(int Lq, int d) {
+  const int need = (Lq + 15) / 16;
+  const int cap = 32 / stream_fwd_ks(d);
+  const int nqb = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
+  return nqb < cap ? nqb : cap;
+}
+
+int stream_fwd_passes(int Lq, int d) {
+  const int rows = 16 * stream_fwd_nqb(Lq, d);
+  return (Lq + rows - 1) / rows;
+}
+
+hipError_t launch_stream_fwd(int kind, const FwdArgs& a, bool with_argmax, hipStream_t s) {
+  switch (kind) {
+    case KIND_F16: return dispatch_ks<KIND_F16>(a, with_argmax, s);
+    case KIND_BF16: return dispatch_ks<KIND_BF16>(a, with_argmax, s);
+    case KIND_U8: return dispatch_ks<KIND_U8>(a, false, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace fmx

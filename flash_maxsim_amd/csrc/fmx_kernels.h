@@ -1,0 +1,69 @@
+// Host-visible kernel launchers of the flash_maxsim MI355X library. The C ABI
+// in fmx_api.cpp validates arguments and picks a launcher; each launcher picks
+// the template instance for the shape and enqueues it on the caller's stream.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fmx {
+
+// One forward call: Nq queries of Lq tokens scored against docs of Ld tokens
+// with d-wide embeddings. Strides are in elements of the operand's type.
+struct FwdArgs {
+  const void* Q;              // [Nq, Lq, d] fp16/bf16, row stride sq_l, query stride sq_n
+  const void* D;              // [B' , Ld, d] fp16/bf16/uint8, strides sd_b, sd_l
+  const int32_t* lengths;     // [B'] valid tokens per doc row, or null (= Ld)
+  float* scores;              // [Nq, B] fp32, strides ss_n, ss_b
+  int32_t* argmax;            // [Nq*B, Lq] int32, or null
+  const uint16_t* scales;     // uint8 docs: fp16 bits [B', Ld], doc stride sm_b, token stride 1
+  const uint16_t* mins;       // uint8 docs: fp16 bits, same layout as scales
+  float* partial;             // workspace: per-pass partial sums [passes, Nq*B]
+  const int32_t* qidx;        // sparse scoring: [B, Lq] rows of Q per doc, or null
+  int64_t si_b, si_k;         // qidx strides
+  int64_t sq_n, sq_l;
+  int64_t sd_b, sd_l;
+  int64_t ss_n, ss_b;
+  int64_t sm_b;
+  int Nq, B, Lq, Ld, d;
+  int Lq_rows;                // rows of Q (= Lq unless qidx gathers from a longer Q)
+  int shared_docs;            // doc row of (query qi, doc b) is b, else qi*B + b
+  int sm_vec;                 // scales/mins may be read 4 tokens per load
+};
+
+// Backward of the single-query forward with saved argmax.
+struct BwdArgs {
+  const void* Q;              // [Lq, d], row stride sq_l
+  const void* D;              // [B, Ld, d], strides sd_b, sd_l
+  const int32_t* argmax;      // [B, Lq]
+  const float* grad;          // [B]
+  void* dQ;                   // [Lq, d] contiguous, or null
+  void* dD;                   // [B, Ld, d] contiguous, or null
+  float* ws;                  // dQ partial sums [nchunk, Lq, d]
+  int64_t sq_l, sd_b, sd_l;
+  int B, Lq, Ld, d;
+  int nchunk;                 // doc chunks of the dQ gather
+};
+
+// Shape class handled by the streaming kernel (query tile in VGPRs, docs read
+// straight from HBM into VGPRs): d <= 256.
+bool stream_fwd_supported(int d);
+int stream_fwd_ks(int d);             // 32-wide k-steps held per fragment row
+int stream_fwd_nqb(int Lq, int d);    // 16-token query blocks per pass
+int stream_fwd_passes(int Lq, int d); // > 1: partial sums in FwdArgs::partial
+hipError_t launch_stream_fwd(int kind, const FwdArgs& a, bool with_argmax, hipStream_t s);
+
+// Split-d kernel: the eight waves of a workgroup each own a slice of d and
+// reduce partial similarities through LDS before the max. 256 < d <= 2048.
+bool splitd_fwd_supported(int d);
+int splitd_fwd_ksw(int d);            // k-steps per wave
+int splitd_fwd_nqb(int Lq, int d);    // 16-token query blocks per pass
+int splitd_fwd_passes(int Lq, int d); // > 1: partial sums in FwdArgs::partial
+hipError_t launch_splitd_fwd(int kind, const FwdArgs& a, bool with_argmax, hipStream_t s);
+
+// dQ / dD of the argmax backward.
+int bwd_dq_chunks(int B, int Lq, int d);
+size_t bwd_dd_lds_bytes(int Lq, int Ld);  // dynamic LDS of the dD kernel
+hipError_t launch_bwd(int kind, const BwdArgs& a, hipStream_t s);
+
+}  // namespace fmx

@@ -1,0 +1,199 @@
+"""MaxSim scoring on MI355X: single-query, batched and training entry points.
+
+Mirrors the public functions of the reference module
+flash_maxsim/flash_maxsim.py (flash_maxsim :221, flash_maxsim_batched :233,
+flash_maxsim_train :289, maxsim_naive :294): same names, positional order,
+defaults, AssertionError on bad ranks/shapes and fp16 casting of inputs. The
+work runs in libflashmaxsim's HIP kernels (include/fmx.h); there is no CPU or
+torch fallback for the flash_* functions.
+
+Differences by design:
+  * bfloat16 Q and D run on the bf16 MFMA as they are instead of being cast to
+    fp16 (any other dtype mix is cast to fp16 as in the reference);
+  * doc_lengths are clamped to [0, Ld] on the GPU (the reference reads past the
+    doc for lengths > Ld) and must have one entry per doc row;
+  * a d that is not a multiple of 8 is zero-padded to one (a copy) because the
+    kernels read rows with 16-byte loads.
+"""
+
+from __future__ import annotations
+
+import contextlib
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+
+
+def _check_devices(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise RuntimeError(f"flash_maxsim_amd runs on a ROCm GPU; got a tensor on {dev}")
+    for t in tensors[1:]:
+        if t is not None and t.device != dev:
+            raise RuntimeError(f"all operands must be on {dev}; got one on {t.device}")
+    return dev
+
+
+def _device_guard(dev: torch.device):
+    if dev.index is None or dev.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(dev)
+
+
+def _kernel_dtype(*tensors: torch.Tensor) -> torch.dtype:
+    """fp16, as the reference's .half() casts, unless every operand is bf16."""
+    return torch.bfloat16 if all(t.dtype == torch.bfloat16 for t in tensors) else torch.float16
+
+
+def _prep(t: torch.Tensor, dtype: torch.dtype | None) -> torch.Tensor:
+    """Contiguous, cast, d padded to a multiple of 8, 16-byte aligned."""
+    t = t.contiguous()
+    if dtype is not None and t.dtype != dtype:
+        t = t.to(dtype)
+    pad = (-t.shape[-1]) % 8
+    if pad:
+        t = F.pad(t, (0, pad))
+    if t.data_ptr() % 16:
+        t = t.clone()
+    return t
+
+
+def _lengths(total: int, device: torch.device, doc_lengths) -> torch.Tensor | None:
+    """int32 doc lengths on the device, or None for full length (reference :211-214)."""
+    if doc_lengths is None:
+        return None
+    lengths = doc_lengths.to(device=device, dtype=torch.int32).contiguous()
+    assert lengths.numel() == total, f"doc_lengths has {lengths.numel()} entries, expected {total}"
+    return lengths
+
+
+def _launch_fwd(Q, D, lengths, Nq, B, Lq, Ld, d, shared_docs, save_argmax):
+    """Scores [Nq, B] fp32 (+ argmax [Nq*B, Lq] int32) from prepared operands.
+
+    Q is [Nq, Lq, dp] or [Lq, dp], D is [B', Ld, dp] with dp = d rounded up to
+    8; mirrors _launch_fwd (reference flash_maxsim.py:195-208).
+    """
+    dev = _check_devices(Q, D, lengths)
+    lib = _lib.load()
+    scores = torch.empty(Nq, B, device=dev, dtype=torch.float32)
+    argmax = torch.empty(Nq * B, Lq, device=dev, dtype=torch.int32) if save_argmax else None
+    if Nq == 0 or B == 0:
+        return scores, argmax
+    if Lq == 0:
+        scores.zero_()
+        return scores, argmax
+    nbytes = lib.fmx_fwd_workspace_bytes(Nq, B, Lq, Ld, d)
+    ws = _lib.workspace(nbytes, dev)
+    q_stride_n = Q.stride(0) if Q.dim() == 3 else 0
+    with _device_guard(dev):
+        rc = lib.fmx_fwd(
+            _lib.dtype_code(Q), Q.data_ptr(), q_stride_n, Q.stride(-2),
+            D.data_ptr(), D.stride(0), D.stride(1), _lib.ptr(lengths),
+            scores.data_ptr(), scores.stride(0), scores.stride(1), _lib.ptr(argmax),
+            Nq, B, Lq, Ld, d, int(bool(shared_docs)), _lib.ptr(ws), nbytes, _lib.stream_of(Q),
+        )
+    _lib.check(rc)
+    return scores, argmax
+
+
+def flash_maxsim(Q: torch.Tensor, D: torch.Tensor, doc_lengths=None) -> torch.Tensor:
+    """Compute MaxSim scores. Q: [Lq, d], D: [B, Ld, d] -> [B]."""
+    assert Q.dim() == 2 and D.dim() == 3 and Q.shape[1] == D.shape[2]
+    Lq, d = Q.shape
+    B, Ld, _ = D.shape
+    dt = _kernel_dtype(Q, D)
+    Q2 = _prep(Q, dt)
+    D2 = _prep(D, dt)
+    lengths = _lengths(B, D.device, doc_lengths)
+    scores, _ = _launch_fwd(Q2.unsqueeze(0), D2, lengths, 1, B, Lq, Ld, d, True, False)
+    return scores.squeeze(0)
+
+
+def flash_maxsim_batched(Q: torch.Tensor, D: torch.Tensor, doc_lengths=None,
+                         shared_docs: bool = True) -> torch.Tensor:
+    """Batched MaxSim. Q: [Nq, Lq, d], D: [B, Ld, d] -> [Nq, B]."""
+    assert Q.dim() == 3 and Q.shape[2] == D.shape[-1]
+    Nq, Lq, d = Q.shape
+    if shared_docs:
+        assert D.dim() == 3
+        B, Ld, _ = D.shape
+    else:
+        assert D.dim() == 4 and D.shape[0] == Nq
+        _, B, Ld, _ = D.shape
+        D = D.reshape(Nq * B, Ld, d)
+    dt = _kernel_dtype(Q, D)
+    Q2 = _prep(Q, dt)
+    D2 = _prep(D, dt)
+    total = B if shared_docs else Nq * B
+    lengths = _lengths(total, D.device, doc_lengths)
+    scores, _ = _launch_fwd(Q2, D2, lengths, Nq, B, Lq, Ld, d, shared_docs, False)
+    return scores
+
+
+class _FlashMaxSimFn(torch.autograd.Function):
+    """Forward saves per-(doc, query token) argmax; backward scatters through it
+    (reference flash_maxsim.py:253-286)."""
+
+    @staticmethod
+    def forward(ctx, Q, D):
+        Lq, d = Q.shape
+        B, Ld, _ = D.shape
+        dt = _kernel_dtype(Q, D)
+        Q2 = _prep(Q, dt)
+        D2 = _prep(D, dt)
+        scores, argmax = _launch_fwd(Q2.unsqueeze(0), D2, None, 1, B, Lq, Ld, d, True, True)
+        ctx.save_for_backward(Q2, D2, argmax)
+        ctx.d = d
+        return scores.squeeze(0)
+
+    @staticmethod
+    def backward(ctx, grad_scores):
+        Q2, D2, argmax = ctx.saved_tensors
+        d = ctx.d
+        Lq = Q2.shape[0]
+        B, Ld, _ = D2.shape
+        need_q, need_d = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        dev = _check_devices(Q2, D2, grad_scores)
+        grad_Q = torch.empty(Lq, d, device=dev, dtype=Q2.dtype) if need_q else None
+        grad_D = torch.empty(B, Ld, d, device=dev, dtype=D2.dtype) if need_d else None
+        if (grad_Q is None and grad_D is None) or Lq == 0:
+            if grad_Q is not None:
+                grad_Q.zero_()
+            if grad_D is not None:
+                grad_D.zero_()
+            return grad_Q, grad_D
+        g = grad_scores.contiguous().float()
+        lib = _lib.load()
+        nbytes = lib.fmx_bwd_workspace_bytes(B, Lq, Ld, d) if need_q else 0
+        ws = _lib.workspace(nbytes, dev)
+        with _device_guard(dev):
+            rc = lib.fmx_bwd(
+                _lib.dtype_code(Q2), Q2.data_ptr(), Q2.stride(0), D2.data_ptr(), D2.stride(0), D2.stride(1),
+                argmax.data_ptr(), g.data_ptr(), _lib.ptr(grad_Q), _lib.ptr(grad_D),
+                B, Lq, Ld, d, _lib.ptr(ws), nbytes, _lib.stream_of(Q2),
+            )
+        _lib.check(rc)
+        return grad_Q, grad_D
+
+
+def flash_maxsim_train(Q: torch.Tensor, D: torch.Tensor) -> torch.Tensor:
+    """MaxSim with autograd backward. Q: [Lq, d], D: [B, Ld, d] -> [B]."""
+    assert Q.dim() == 2 and D.dim() == 3 and Q.shape[1] == D.shape[2]
+    return _FlashMaxSimFn.apply(Q, D)
+
+
+def maxsim_naive(Q: torch.Tensor, D: torch.Tensor, doc_lengths=None) -> torch.Tensor:
+    """Reference PyTorch MaxSim. Q: [Lq, d], D: [B, Ld, d] -> [B].
+
+    Plain torch in fp32 (reference flash_maxsim.py:294-301): S = D Q^T, tokens
+    at or past doc_lengths masked to -inf, max over doc tokens, sum over query
+    tokens. Runs wherever its inputs live.
+    """
+    S = torch.matmul(D.float(), Q.float().t().contiguous())  # [B, Ld, Lq]
+    if doc_lengths is not None:
+        Ld = D.shape[1]
+        pos = torch.arange(Ld, device=D.device)[None, :, None]
+        S = S.masked_fill(pos >= doc_lengths.to(D.device)[:, None, None], float("-inf"))
+    return S.max(dim=1).values.sum(dim=1)

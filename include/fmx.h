@@ -1,0 +1,140 @@
+/*
+ * fmx.h - C ABI of libflashmaxsim, the MI355X (gfx950) MaxSim scoring library.
+ *
+ * The reference (roipony/flash-maxsim 0.1.0) exposes this path only as a
+ * Python API over Triton launches; each entry point below is the native
+ * boundary under one of its Python functions, which keep their signatures,
+ * asserts and casts in the flash_maxsim_amd package.
+ *
+ * Conventions (all entry points):
+ *  - Every tensor pointer is a device pointer owned by the caller. The library
+ *    allocates nothing; scratch space is a caller-provided workspace whose size
+ *    the matching *_workspace_bytes() function returns (0 means none needed).
+ *  - Strides are in elements of the tensor's type. The innermost (d) stride is
+ *    1. Row strides of Q and D must be multiples of 8 elements, doc strides of
+ *    D multiples of 8, and Q, D 16-byte aligned; d itself may be anything
+ *    from 1 to FMX_MAX_D (elements past d in a row are never used).
+ *  - `stream` is a hipStream_t (NULL = the default stream). Work is enqueued
+ *    asynchronously; nothing synchronises the host.
+ *  - Return value: FMX_OK, or a negative FMX_ERR_* code with a message
+ *    available from fmx_last_error() on the calling thread.
+ *  - Doc lengths are clamped to [0, Ld]; a doc with no valid token scores
+ *    -inf (every similarity is masked), and its argmax entries are 0.
+ */
+#ifndef FMX_H_
+#define FMX_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FMX_OK 0
+#define FMX_ERR_INVALID (-1)      /* bad shape, stride, alignment or pointer */
+#define FMX_ERR_UNSUPPORTED (-2)  /* valid but outside what the kernels cover */
+#define FMX_ERR_WORKSPACE (-3)    /* workspace missing or too small */
+#define FMX_ERR_HIP (-4)          /* a HIP runtime call failed */
+
+#define FMX_DTYPE_F16 0
+#define FMX_DTYPE_BF16 1
+
+#define FMX_MAX_D 2048
+
+/* Library version string ("0.1.0+mi355x"). */
+const char* fmx_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* fmx_last_error(void);
+
+/*
+ * MaxSim forward: scores[qi, b] = sum_{q < Lq} max_{j < len} <Q[qi, q], D[row, j]>
+ * with row = b if shared_docs else qi*B + b, and len = lengths[row] (Ld if
+ * lengths is NULL). fp16/bf16 inputs, fp32 accumulation and output.
+ *
+ *   Q        [Nq, Lq, d]   dtype, strides (q_stride_n, q_stride_l, 1)
+ *   D        [B', Ld, d]   dtype, strides (d_stride_b, d_stride_l, 1); B' = B or Nq*B
+ *   lengths  [B']          int32, or NULL
+ *   scores   [Nq, B]       fp32, strides (s_stride_n, s_stride_b)
+ *   argmax   [Nq*B, Lq]    int32, or NULL; row qi*B + b holds, per query token,
+ *                          the first doc token reaching the max
+ *
+ * Replaces flash_maxsim/flash_maxsim.py:195-208 (_launch_fwd) and the kernel
+ * it launches, _maxsim_fwd_kernel (flash_maxsim.py:80-146); called by the
+ * Python flash_maxsim (flash_maxsim.py:221-230), flash_maxsim_batched
+ * (:233-250) and flash_maxsim_train's forward (:254-263).
+ */
+int fmx_fwd(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, const void* D,
+            int64_t d_stride_b, int64_t d_stride_l, const int32_t* lengths, float* scores,
+            int64_t s_stride_n, int64_t s_stride_b, int32_t* argmax, int64_t Nq, int64_t B,
+            int64_t Lq, int64_t Ld, int64_t d, int shared_docs, void* workspace,
+            size_t workspace_bytes, void* stream);
+
+size_t fmx_fwd_workspace_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t Ld, int64_t d);
+
+/*
+ * Fused uint8-dequant MaxSim forward: doc token j of doc b is
+ * code * scales[b, j] + mins[b, j] (per-token affine, fp16 scale and min).
+ *
+ *   Q        [Lq, d]   fp16, row stride q_stride_l
+ *   D        [B, Ld, d] uint8 codes, strides (d_stride_b, d_stride_l, 1)
+ *   scales   [B, Ld]   fp16, strides (sm_stride_b, 1)
+ *   mins     [B, Ld]   fp16, strides (sm_stride_b, 1)
+ *   lengths  [B]       int32, or NULL
+ *   scores   [B]       fp32, contiguous
+ *
+ * Replaces flash_maxsim/flash_maxsim_quant.py:135-141 (the launch in
+ * flash_maxsim_int8) and _maxsim_int8_kernel (flash_maxsim_quant.py:40-98).
+ */
+int fmx_fwd_int8(const void* Q, int64_t q_stride_l, const uint8_t* D, int64_t d_stride_b,
+                 int64_t d_stride_l, const void* scales, const void* mins, int64_t sm_stride_b,
+                 const int32_t* lengths, float* scores, int64_t B, int64_t Lq, int64_t Ld, int64_t d,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+size_t fmx_fwd_int8_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld, int64_t d);
+
+/*
+ * Sparse MaxSim forward: doc b is scored with its own K query tokens,
+ * scores[b] = sum_{k < K} max_{j < len} <Q[indices[b, k]], D[b, j]>.
+ * An index outside [0, Lq) selects a zero query token.
+ *
+ *   Q        [Lq, d]   dtype, row stride q_stride_l
+ *   D        [B, Ld, d] dtype, strides (d_stride_b, d_stride_l, 1)
+ *   indices  [B, K]    int32, strides (idx_stride_b, idx_stride_k)
+ *   lengths  [B]       int32, or NULL
+ *   scores   [B]       fp32, contiguous
+ *
+ * Replaces flash_maxsim/flash_maxsim_sparse.py:131-139 (the launch in
+ * flash_maxsim_sparse) and _sparse_maxsim_kernel (flash_maxsim_sparse.py:28-91).
+ */
+int fmx_fwd_sparse(int dtype, const void* Q, int64_t q_stride_l, int64_t Lq, const void* D,
+                   int64_t d_stride_b, int64_t d_stride_l, const int32_t* indices, int64_t idx_stride_b,
+                   int64_t idx_stride_k, int64_t K, const int32_t* lengths, float* scores, int64_t B,
+                   int64_t Ld, int64_t d, void* workspace, size_t workspace_bytes, void* stream);
+
+size_t fmx_fwd_sparse_workspace_bytes(int64_t B, int64_t K, int64_t Ld, int64_t d);
+
+/*
+ * Argmax backward of the single-query forward (argmax from fmx_fwd, Nq = 1):
+ *   dQ[q, :]    = sum_b grad[b] * D[b, argmax[b, q], :]
+ *   dD[b, j, :] = grad[b] * sum_{q : argmax[b, q] = j} Q[q, :]
+ * dQ ([Lq, d]) and dD ([B, Ld, d]) are written contiguous in `dtype`, each
+ * skipped when NULL. dD is fully written (zeros where no token picked a row).
+ *
+ * Replaces flash_maxsim/flash_maxsim.py:265-286 (_FlashMaxSimFn.backward) and
+ * its kernels _maxsim_bwd_dQ_kernel (:153-168) and _maxsim_bwd_dD_kernel
+ * (:171-188).
+ */
+int fmx_bwd(int dtype, const void* Q, int64_t q_stride_l, const void* D, int64_t d_stride_b,
+            int64_t d_stride_l, const int32_t* argmax, const float* grad_scores, void* dQ, void* dD,
+            int64_t B, int64_t Lq, int64_t Ld, int64_t d, void* workspace, size_t workspace_bytes,
+            void* stream);
+
+size_t fmx_bwd_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld, int64_t d);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FMX_H_ */

@@ -1,0 +1,174 @@
+"""CPU-side checks of the boundary: the C ABI library and the Python API.
+
+No kernel runs here. The library must load, export every entry point that
+include/fmx.h declares (with the arity the ctypes binding uses), and reject
+bad arguments with the documented error codes before any launch. The Python
+API must raise the reference's AssertionError on bad ranks/shapes and refuse
+CPU tensors instead of falling back to a CPU path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from flash_maxsim_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "fmx.h"
+
+FMX_OK, FMX_ERR_INVALID, FMX_ERR_UNSUPPORTED, FMX_ERR_WORKSPACE = 0, -1, -2, -3
+
+
+def _header_decls():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    decls = {}
+    for m in re.finditer(r"\b(fmx_\w+)\s*\(([^)]*)\)\s*;", text):
+        args = m.group(2).strip()
+        decls[m.group(1)] = 0 if args in ("", "void") else len(args.split(","))
+    return decls
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_header_and_binding_agree(lib):
+    decls = _header_decls()
+    assert decls, "no declarations parsed from include/fmx.h"
+    assert set(decls) == set(_lib.EXPORTED)
+    for name, nargs in decls.items():
+        assert len(_lib._SIGNATURES[name][1]) == nargs, name
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _header_decls():
+        assert hasattr(lib, name), f"libflashmaxsim.so does not export {name}"
+
+
+def test_version(lib):
+    assert lib.fmx_version().decode() == "0.1.0+mi355x"
+
+
+FAKE = 0x10000  # aligned, never dereferenced: every call below fails validation first
+
+
+def _fwd(lib, **kw):
+    a = dict(dtype=0, Q=FAKE, qn=0, ql=128, D=FAKE, db=300 * 128, dl=128, lengths=None, scores=FAKE,
+             sn=0, sb=1, argmax=None, Nq=1, B=10, Lq=32, Ld=300, d=128, shared=1, ws=None, wsb=0)
+    a.update(kw)
+    return lib.fmx_fwd(a["dtype"], a["Q"], a["qn"], a["ql"], a["D"], a["db"], a["dl"], a["lengths"],
+                       a["scores"], a["sn"], a["sb"], a["argmax"], a["Nq"], a["B"], a["Lq"], a["Ld"],
+                       a["d"], a["shared"], a["ws"], a["wsb"], None)
+
+
+@pytest.mark.parametrize("kw, code, text", [
+    (dict(dtype=7), FMX_ERR_INVALID, "dtype"),
+    (dict(d=4096, ql=4096, dl=4096, db=4096 * 300), FMX_ERR_UNSUPPORTED, "FMX_MAX_D"),
+    (dict(ql=100), FMX_ERR_INVALID, "Q row stride"),
+    (dict(dl=120), FMX_ERR_INVALID, "D row stride"),
+    (dict(db=300 * 128 + 4), FMX_ERR_INVALID, "doc stride"),
+    (dict(Lq=0), FMX_ERR_INVALID, "invalid sizes"),
+    (dict(Q=FAKE + 2), FMX_ERR_INVALID, "aligned"),
+    (dict(Q=None), FMX_ERR_INVALID, "non-null"),
+    (dict(Lq=1024), FMX_ERR_WORKSPACE, "workspace"),
+    (dict(Ld=2**24), FMX_ERR_UNSUPPORTED, "exceeds 2 GiB"),
+])
+def test_fwd_rejects_bad_arguments(lib, kw, code, text):
+    assert _fwd(lib, **kw) == code
+    assert text in lib.fmx_last_error().decode()
+
+
+def test_fwd_empty_batch_is_a_no_op(lib):
+    assert _fwd(lib, B=0, Q=None, D=None, scores=None) == FMX_OK
+    assert lib.fmx_last_error().decode() == ""
+
+
+def test_workspace_sizes(lib):
+    # Lq <= 128 at d <= 256 runs in one pass: no workspace.
+    assert lib.fmx_fwd_workspace_bytes(1, 5000, 32, 300, 128) == 0
+    assert lib.fmx_fwd_workspace_bytes(100, 5000, 32, 300, 128) == 0
+    # Lq = 1024 at d = 128: 8 passes of 128 query tokens.
+    assert lib.fmx_fwd_workspace_bytes(1, 10, 1024, 64, 128) == 8 * 10 * 4
+    # d = 1024 (split-d): 8 query blocks of 16 per pass -> Lq = 128 in one pass.
+    assert lib.fmx_fwd_workspace_bytes(1, 1000, 128, 512, 1024) == 0
+    assert lib.fmx_fwd_int8_workspace_bytes(5000, 32, 1024, 128) == 0
+    assert lib.fmx_bwd_workspace_bytes(1000, 128, 512, 1024) > 0
+
+
+def test_int8_and_bwd_reject_bad_arguments(lib):
+    rc = lib.fmx_fwd_int8(FAKE, 128, FAKE, 300 * 128, 128, FAKE + 1, FAKE, 300, None, FAKE,
+                          10, 32, 300, 128, None, 0, None)
+    assert rc == FMX_ERR_INVALID and "2-byte aligned" in lib.fmx_last_error().decode()
+    rc = lib.fmx_bwd(0, FAKE, 128, FAKE, 300 * 128, 128, FAKE, FAKE, FAKE, None, 10, 32, 300, 128,
+                     None, 0, None)
+    assert rc == FMX_ERR_WORKSPACE
+    rc = lib.fmx_bwd(0, FAKE, 128, FAKE, 300 * 128, 128, FAKE, FAKE, None, None, 10, 32, 300, 128,
+                     None, 0, None)
+    assert rc == FMX_OK  # nothing requested
+
+
+def test_sparse_rejects_bad_arguments(lib):
+    rc = lib.fmx_fwd_sparse(0, FAKE, 128, 32, FAKE, 300 * 128, 128, None, 16, 1, 16, None, FAKE,
+                            10, 300, 128, None, 0, None)
+    assert rc == FMX_ERR_INVALID and "indices" in lib.fmx_last_error().decode()
+
+
+# ---------------------------------------------------------- Python API ----
+
+def test_python_api_asserts_like_the_reference():
+    import flash_maxsim_amd as fm
+
+    Q, D = torch.zeros(4, 8), torch.zeros(2, 5, 8)
+    with pytest.raises(AssertionError):
+        fm.flash_maxsim(Q[None], D)
+    with pytest.raises(AssertionError):
+        fm.flash_maxsim(Q, D[..., :4])
+    with pytest.raises(AssertionError):
+        fm.flash_maxsim_batched(Q, D)
+    with pytest.raises(AssertionError):
+        fm.flash_maxsim_batched(Q[None], D[None], shared_docs=True)
+    with pytest.raises(AssertionError):
+        fm.flash_maxsim_batched(Q[None].expand(2, 4, 8), D[None], shared_docs=False)
+    with pytest.raises(AssertionError):
+        fm.flash_maxsim_int8(Q, torch.zeros(2, 5, 8, dtype=torch.uint8)[0], torch.zeros(2, 5), torch.zeros(2, 5))
+    with pytest.raises(AssertionError):
+        fm.flash_maxsim_sparse(Q, D, torch.zeros(3, 2, dtype=torch.int32))
+    with pytest.raises(AssertionError):
+        fm.quantize_int8(D[0])
+
+
+def test_python_api_refuses_cpu_tensors():
+    import flash_maxsim_amd as fm
+
+    Q, D = torch.zeros(4, 8, dtype=torch.float16), torch.zeros(2, 5, 8, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        fm.flash_maxsim(Q, D)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        fm.flash_maxsim_train(Q, D)
+
+
+def test_naive_functions_run_on_cpu():
+    import flash_maxsim_amd as fm
+
+    Q = torch.randn(4, 8)
+    D = torch.randn(3, 5, 8)
+    s = fm.maxsim_naive(Q, D, torch.tensor([5, 2, 0]))
+    assert s.shape == (3,) and torch.isinf(s[2]) and s[2] < 0
+    codes, sc, mn = fm.quantize_int8(D)
+    assert codes.dtype == torch.uint8 and sc.shape == (3, 5, 1) and mn.dtype == torch.float16
+    assert fm.dequantize_int8(codes, sc, mn).shape == D.shape
+    idx = torch.tensor([[0, 1], [2, 3], [3, 3]])
+    assert fm.maxsim_sparse_naive(Q, D, idx).shape == (3,)
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libflashmaxsim.so")
+    with pytest.raises(RuntimeError, match="missing"):
+        _lib.load()
