@@ -135,6 +135,15 @@ def make_workload(name):
             oracle.bwd(Qn, Dn, am, np.ones(4))
 
         return cfg, step, B, roof, oracle_fn, 4, "docs/s"
+    if name == "copy":
+        # Calibration for HBM byte counters: a plain device copy of the metric's D size.
+        n = 5000 * 300 * 128
+        src = torch.empty(n, dtype=torch.float16, device=dev).normal_()
+        dst = torch.empty_like(src)
+        cfg = {"workload": f"device copy of {n * 2} bytes (counter calibration)", "bytes": n * 2}
+        step = lambda: dst.copy_(src)  # noqa: E731
+        roof = {"bound": "hbm", "amount": 2 * n * 2, "unit": "GB/s", "kernel": "copy"}
+        return cfg, step, 1, roof, (lambda: None), 1, "copies/s"
     raise SystemExit(f"unknown config {name}")
 
 
@@ -153,7 +162,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="c1")
+    ap.add_argument("--config", default="c1", help="c1 (metric), c1_1000, c2, c3, c4, c5, copy")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -199,7 +208,7 @@ def main():
                 "kernel_ms": round(kern_ms, 5), "kernel_ms_median": round(float(np.median(per)), 5)}
 
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and args.config != "copy":
         threads = oracle.default_threads()
         oracle_fn()  # warm
         times = []
