@@ -147,6 +147,19 @@ def make_workload(name):
     raise SystemExit(f"unknown config {name}")
 
 
+def measured_traffic(config: str):
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 --pmc
+    summaries in profiles/ (line `traffic_bytes_per_launch[<config>] = N`), or None."""
+    import re
+
+    pat = re.compile(r"^traffic_bytes_per_launch\[" + re.escape(config) + r"\]\s*=\s*(\d+)", re.M)
+    for f in sorted((ROOT / "profiles").glob("*.md")):
+        m = pat.search(f.read_text())
+        if m:
+            return int(m.group(1)), f"profiles/{f.name}"
+    return None, None
+
+
 def cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -203,8 +216,10 @@ def main():
     else:
         achieved /= 1e12
         peak = MFMA_F16_PEAK_TFLOPS
+    traffic, traffic_src = measured_traffic(args.config)
     roofline = {"bound": roof["bound"], "achieved": round(achieved, 2), "peak": peak, "unit": roof["unit"],
-                "frac": round(achieved / peak, 4), "traffic": None, "kernel": roof["kernel"],
+                "frac": round(achieved / peak, 4), "traffic": traffic, "traffic_source": traffic_src,
+                "algorithmic": roof["amount"], "kernel": roof["kernel"],
                 "kernel_ms": round(kern_ms, 5), "kernel_ms_median": round(float(np.median(per)), 5)}
 
     cpu = None
