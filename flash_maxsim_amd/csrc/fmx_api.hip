@@ -45,10 +45,41 @@ FwdPlan plan_fwd(int64_t Lq, int64_t d) {
   return p;
 }
 
-size_t fwd_ws_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t d) {
+// Compute units of the current device (cached per device; 256 if unknown).
+int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+// Whether fmx_fwd takes the tiled (MFMA-bound) kernel for this call.
+bool use_tiled(int64_t Nq, int64_t Lq, int64_t d, int shared_docs) {
+  return (shared_docs || Nq == 1) && fmx::tiled_fwd_applicable(Nq, Lq, (int)d);
+}
+
+// Streaming / split-d kernels: per-pass partial sums when the query needs
+// several passes.
+size_t stream_ws_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t d) {
   if (Lq < 1 || d < 1 || d > FMX_MAX_D || Nq < 1 || B < 1) return 0;
   const FwdPlan p = plan_fwd(Lq, d);
   return p.passes > 1 ? (size_t)p.passes * (size_t)Nq * (size_t)B * sizeof(float) : 0;
+}
+
+// Upper bound over the kernels fmx_fwd may pick for these sizes.
+size_t fwd_ws_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t d) {
+  size_t n = stream_ws_bytes(Nq, B, Lq, d);
+  if (Nq >= 1 && B >= 1 && Lq >= 1 && fmx::tiled_fwd_applicable(Nq, Lq, (int)d)) {
+    const fmx::TiledPlan p = fmx::tiled_fwd_plan(Nq, B, Lq, (int)d, device_cus());
+    const size_t t = fmx::tiled_fwd_workspace_bytes(p, Nq, B);
+    if (t > n) n = t;
+  }
+  return n;
 }
 
 // Checks shared by the forward entry points. esz: bytes per D element.
@@ -93,7 +124,7 @@ size_t fmx_fwd_workspace_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t Ld, in
 
 size_t fmx_fwd_int8_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld, int64_t d) {
   (void)Ld;
-  return fwd_ws_bytes(1, B, Lq, d);
+  return stream_ws_bytes(1, B, Lq, d);
 }
 
 int fmx_fwd(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, const void* D,
@@ -108,7 +139,15 @@ int fmx_fwd(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, co
   if (!Q || !D || !scores) return fail(FMX_ERR_INVALID, "Q, D and scores must be non-null");
   if (!aligned16(Q) || !aligned16(D)) return fail(FMX_ERR_INVALID, "Q and D must be 16-byte aligned");
   if (Nq > 1 && (q_stride_n & 7)) return fail(FMX_ERR_INVALID, "Q query stride must be a multiple of 8");
-  const size_t need = fwd_ws_bytes(Nq, B, Lq, d);
+  const bool tiled = use_tiled(Nq, Lq, d, shared_docs);
+  fmx::TiledPlan tp = {};
+  size_t need;
+  if (tiled) {
+    tp = fmx::tiled_fwd_plan(Nq, B, Lq, (int)d, device_cus());
+    need = fmx::tiled_fwd_workspace_bytes(tp, Nq, B);
+  } else {
+    need = stream_ws_bytes(Nq, B, Lq, d);
+  }
   if (need > 0 && (!workspace || workspace_bytes < need))
     return fail(FMX_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
 
@@ -134,8 +173,14 @@ int fmx_fwd(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, co
   a.shared_docs = shared_docs ? 1 : 0;
   const int kind = dtype == FMX_DTYPE_BF16 ? fmx::KIND_BF16 : fmx::KIND_F16;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const hipError_t e = plan_fwd(Lq, d).splitd ? fmx::launch_splitd_fwd(kind, a, argmax != nullptr, s)
-                                              : fmx::launch_stream_fwd(kind, a, argmax != nullptr, s);
+  hipError_t e;
+  if (tiled) {
+    e = fmx::launch_tiled_fwd(kind, a, tp, argmax != nullptr, s);
+  } else if (plan_fwd(Lq, d).splitd) {
+    e = fmx::launch_splitd_fwd(kind, a, argmax != nullptr, s);
+  } else {
+    e = fmx::launch_stream_fwd(kind, a, argmax != nullptr, s);
+  }
   return hip_status(e, "fmx_fwd launch");
 }
 
@@ -152,7 +197,7 @@ int fmx_fwd_int8(const void* Q, int64_t q_stride_l, const uint8_t* D, int64_t d_
   if ((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(mins)) & 1u)
     return fail(FMX_ERR_INVALID, "scales and mins must be 2-byte aligned");
   if (sm_stride_b < Ld) return fail(FMX_ERR_INVALID, "scale doc stride %lld < Ld", (long long)sm_stride_b);
-  const size_t need = fwd_ws_bytes(1, B, Lq, d);
+  const size_t need = stream_ws_bytes(1, B, Lq, d);
   if (need > 0 && (!workspace || workspace_bytes < need))
     return fail(FMX_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
 
@@ -193,7 +238,7 @@ int fmx_fwd_int8(const void* Q, int64_t q_stride_l, const uint8_t* D, int64_t d_
 
 size_t fmx_fwd_sparse_workspace_bytes(int64_t B, int64_t K, int64_t Ld, int64_t d) {
   (void)Ld;
-  return fwd_ws_bytes(1, B, K, d);
+  return stream_ws_bytes(1, B, K, d);
 }
 
 int fmx_fwd_sparse(int dtype, const void* Q, int64_t q_stride_l, int64_t Lq, const void* D,
@@ -208,7 +253,7 @@ int fmx_fwd_sparse(int dtype, const void* Q, int64_t q_stride_l, int64_t Lq, con
   if (B == 0) return ok();
   if (!Q || !D || !scores || !indices) return fail(FMX_ERR_INVALID, "Q, D, indices and scores must be non-null");
   if (!aligned16(Q) || !aligned16(D)) return fail(FMX_ERR_INVALID, "Q and D must be 16-byte aligned");
-  const size_t need = fwd_ws_bytes(1, B, K, d);
+  const size_t need = stream_ws_bytes(1, B, K, d);
   if (need > 0 && (!workspace || workspace_bytes < need))
     return fail(FMX_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
 

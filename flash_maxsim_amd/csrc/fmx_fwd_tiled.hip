@@ -1,0 +1,395 @@
+// Tiled MaxSim forward for many query rows (MFMA-bound regime), d <= 256.
+//
+// Same contract as _maxsim_fwd_kernel (reference flash_maxsim/flash_maxsim.py:
+// 80-146) for single queries with long Lq (config 2: Lq = 1024) and for
+// batched scoring (flash_maxsim.py:233-250, config 3), where the reference
+// re-streams every doc once per (query, 16..128-token block).
+//
+// The Nq*Lq query rows are flattened and cut into row blocks of 8 waves x
+// 16*NB rows. A persistent workgroup of eight waves keeps its row block in
+// VGPRs as MFMA B-fragments and walks a fixed set of docs (doc group g: docs
+// g, g+G, g+2G, ...). Each doc streams in 64-token tiles: global -> VGPR
+// staging -> LDS (double-buffered, rows padded by 16 bytes so the 16 rows of a
+// fragment read fall in distinct banks), then every wave reads the A-fragments
+// of each 16-token subtile from LDS and runs NB*KS MFMAs against its rows,
+// folding the results into per-row running maxima (+ first index). The next
+// tile's global loads are in flight while the current one computes; the tile
+// sequence runs across doc boundaries without draining.
+// At a doc's last tile the row maxima go to LDS (double-buffered by doc
+// parity) and, after the tile barrier, each wave sums the rows of its queries:
+// a query inside the row block is written to scores, a query straddling row
+// blocks to a partial slot that a second kernel adds in row-block order.
+//
+// blockIdx -> (row block, doc group) is XCD-aware when G % 8 == 0: the eight
+// XCDs take workgroups round-robin, so all row blocks of doc group g are put on
+// XCD g % 8 and read each doc tile through the same L2.
+#include "fmx_kernels.h"
+#include "fmx_tile.h"
+
+namespace fmx {
+namespace {
+
+constexpr int kTiledWaves = 8;
+constexpr int kTileTokens = 64;
+
+// A-fragments of 16-token subtile s from an LDS tile with ROWB-byte rows.
+template <int KS, int ROWB>
+__device__ __forceinline__ void read_frags(u32x4_t (&af)[KS], const unsigned char* base, int s, int c, int g) {
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk)
+    af[kk] = *reinterpret_cast<const u32x4_t*>(base + (s * 16 + c) * ROWB + kk * 64 + g * 16);
+}
+
+// S for one subtile against every query block of the wave; k-step outer so the
+// NB accumulation chains are independent and issue back to back.
+template <bool BF, int NB, int KS>
+__device__ __forceinline__ void subtile_mfma(const u32x4_t (&af)[KS], const u32x4_t (&qf)[NB][KS],
+                                             f32x4_t (&acc)[NB]) {
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma16x16x32<BF>(af[kk], qf[nb][kk], acc[nb]);
+  }
+}
+
+// Running max (and first index) of one result fragment: rows rowj .. rowj+3.
+template <bool ARGMAX>
+__device__ __forceinline__ void fold_rows(f32x4_t acc, int rowj, int len, bool tail, float& m, int& mi) {
+  if (tail) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (rowj + i >= len) acc[i] = -INFINITY;
+  }
+  if constexpr (ARGMAX) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (acc[i] > m) {
+        m = acc[i];
+        mi = rowj + i;
+      }
+    }
+  } else {
+    m = fmaxf(m, fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3])));
+  }
+}
+
+template <int KIND, int NB, int KS, bool KMASK, bool ARGMAX>
+__global__ void __launch_bounds__(512) tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
+  constexpr int NW = kTiledWaves, TJ = kTileTokens;
+  constexpr int ROWB = 64 * KS + 16;       // LDS bytes per token row (16 B pad)
+  constexpr int BUFB = TJ * ROWB;          // LDS bytes per tile buffer
+  constexpr int CPR = 4 * KS;              // 16-byte chunks per token row
+  constexpr int CPT = TJ * CPR / (NW * 64);  // chunks per thread per tile
+  constexpr int R = NW * NB * 16;          // rows per row block
+  constexpr bool BF = KindInfo<KIND>::bf;
+  static_assert(CPT * NW * 64 == TJ * CPR, "tile must split evenly over the workgroup");
+  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * BUFB];
+  __shared__ float rowmax[2][R];
+  __shared__ int rowidx[ARGMAX ? 2 : 1][ARGMAX ? R : 1];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15, g = lane >> 4;
+
+  int rb, grp;
+  if (xcd_map) {
+    const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
+    rb = k % nRB;
+    grp = x + 8 * (k / nRB);
+  } else {
+    rb = blockIdx.x % nRB;
+    grp = blockIdx.x / nRB;
+  }
+  if (grp >= G || grp >= a.B) return;
+
+  const int64_t rows_total = (int64_t)a.Nq * a.Lq;
+  const int64_t row0 = (int64_t)rb * R;
+  const int64_t row_end = row0 + R < rows_total ? row0 + R : rows_total;
+
+  // Partial 8-wide group when d % 8 != 0.
+  const int kp = a.d & ~7;
+  const bool has_partial = KMASK && (a.d & 7) != 0;
+
+  // ---- this wave's query rows (B operand), loaded once ----
+  u32x4_t qf[NB][KS];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int64_t r = row0 + wave * NB * 16 + nb * 16 + c;
+    const bool rv = r < rows_total;
+    const int64_t qi = rv ? r / a.Lq : 0;
+    const int64_t q = rv ? r - qi * a.Lq : 0;
+    const uint16_t* qrow = static_cast<const uint16_t*>(a.Q) + qi * a.sq_n + q * a.sq_l;
+#pragma unroll
+    for (int t = 0; t < KS; ++t) {
+      const int k0 = 32 * t + 8 * g;
+      u32x4_t v = {0u, 0u, 0u, 0u};
+      if (rv && (!KMASK || k0 < a.d)) v = *reinterpret_cast<const u32x4_t*>(qrow + k0);
+      if (has_partial && k0 == kp) v &= prefix_mask16(a.d & 7);
+      qf[nb][t] = v;
+    }
+  }
+
+  // ---- tile loader: chunk k of this thread = tid + k*512 -> (row, 16-byte column) ----
+  const uint32_t rowb = (uint32_t)(a.sd_l * 2);
+  auto tile_rsrc = [&](int b, int len) {
+    return make_rsrc(static_cast<const char*>(a.D) + (int64_t)b * a.sd_b * 2, (uint32_t)len * rowb);
+  };
+  auto doc_len = [&](int b) {
+    int l = a.lengths ? a.lengths[b] : a.Ld;
+    return l < 0 ? 0 : (l > a.Ld ? a.Ld : l);
+  };
+  u32x4_t stage[CPT];
+  auto load_tile_regs = [&](rsrc_t rd, int t) {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int chunk = tid + k * NW * 64;
+      const int row = chunk / CPR, cc = chunk - (chunk / CPR) * CPR;
+      const int e0 = cc * 8;
+      uint32_t off = (uint32_t)(t * TJ + row) * rowb + (uint32_t)(e0 * 2);
+      if (KMASK && e0 >= a.d) off = kOOB;
+      stage[k] = ld16(rd, off);
+      if (has_partial && e0 == kp) stage[k] &= prefix_mask16(a.d & 7);
+    }
+  };
+  auto store_tile_lds = [&](int buf) {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int chunk = tid + k * NW * 64;
+      const int row = chunk / CPR, cc = chunk - (chunk / CPR) * CPR;
+      *reinterpret_cast<u32x4_t*>(lds + buf * BUFB + row * ROWB + cc * 16) = stage[k];
+    }
+  };
+
+  float m[NB];
+  int mi[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    m[nb] = -INFINITY;
+    mi[nb] = 0;
+  }
+
+  // ---- doc / tile walk ----
+  int b = grp;
+  int len = doc_len(b);
+  int nt = len > 0 ? (len + TJ - 1) / TJ : 1;  // an empty doc still takes one fully masked tile
+  rsrc_t rd = tile_rsrc(b, len);
+  load_tile_regs(rd, 0);
+  store_tile_lds(0);
+  __syncthreads();
+  int buf = 0, t = 0, par = 0;
+  while (true) {
+    int nb_doc = b, nt_tile = t + 1, nlen = len;
+    if (nt_tile >= nt) {
+      nb_doc = b + G;
+      nt_tile = 0;
+    }
+    const bool has_next = nb_doc < a.B;
+    rsrc_t rd_next = rd;
+    if (has_next) {
+      if (nb_doc != b) {
+        nlen = doc_len(nb_doc);
+        rd_next = tile_rsrc(nb_doc, nlen);
+      }
+      load_tile_regs(rd_next, nt_tile);
+    }
+
+    // compute tile t of doc b from lds[buf]
+    const int j0 = t * TJ;
+    const unsigned char* base = lds + buf * BUFB;
+    if (j0 + TJ <= len) {
+      // full tile: branch-free, A-fragments of subtile s+1 read while s computes
+      u32x4_t af[2][KS];
+      read_frags<KS, ROWB>(af[0], base, 0, c, g);
+#pragma unroll
+      for (int s = 0; s < TJ / 16; ++s) {
+        if (s + 1 < TJ / 16) read_frags<KS, ROWB>(af[(s + 1) & 1], base, s + 1, c, g);
+        f32x4_t acc[NB];
+        subtile_mfma<BF, NB, KS>(af[s & 1], qf, acc);
+        const int rowj = j0 + s * 16 + 4 * g;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) fold_rows<ARGMAX>(acc[nb], rowj, len, false, m[nb], mi[nb]);
+      }
+    } else {
+      // a doc's last, partial tile: skip subtiles past len, mask rows past len
+#pragma unroll
+      for (int s = 0; s < TJ / 16; ++s) {
+        if (j0 + s * 16 < len) {
+          u32x4_t af[KS];
+          read_frags<KS, ROWB>(af, base, s, c, g);
+          f32x4_t acc[NB];
+          subtile_mfma<BF, NB, KS>(af, qf, acc);
+          const int rowj = j0 + s * 16 + 4 * g;
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) fold_rows<ARGMAX>(acc[nb], rowj, len, true, m[nb], mi[nb]);
+        }
+      }
+    }
+
+    const bool last = t + 1 >= nt;
+    if (last) {
+      // row maxima of doc b -> rowmax[par]
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        float v = m[nb];
+        int ix = mi[nb];
+#pragma unroll
+        for (int sh = 16; sh <= 32; sh <<= 1) {
+          const float ov = __shfl_xor(v, sh);
+          if constexpr (ARGMAX) {
+            const int oi = __shfl_xor(ix, sh);
+            argmax_merge(v, ix, ov, oi);
+          } else {
+            v = fmaxf(v, ov);
+          }
+        }
+        if (g == 0) {
+          rowmax[par][wave * NB * 16 + nb * 16 + c] = v;
+          if constexpr (ARGMAX) rowidx[par][wave * NB * 16 + nb * 16 + c] = ix;
+        }
+        m[nb] = -INFINITY;
+        mi[nb] = 0;
+      }
+    }
+    if (has_next) store_tile_lds(buf ^ 1);
+    __syncthreads();
+
+    if (last) {
+      // per-query sums of doc b over this row block
+      const int64_t qfirst = row0 / a.Lq, qlast = (row_end - 1) / a.Lq;
+      for (int64_t qi = qfirst + wave; qi <= qlast; qi += NW) {
+        const int64_t ra = qi * a.Lq > row0 ? qi * a.Lq : row0;
+        const int64_t rz = (qi + 1) * a.Lq < row_end ? (qi + 1) * a.Lq : row_end;
+        float sum = 0.f;
+        for (int64_t r = ra + lane; r < rz; r += 64) {
+          sum += rowmax[par][r - row0];
+          if constexpr (ARGMAX) a.argmax[(qi * a.B + b) * a.Lq + (r - qi * a.Lq)] = rowidx[par][r - row0];
+        }
+        sum = wave_sum(sum);
+        if (lane == 0) {
+          const bool whole = ra == qi * a.Lq && rz == (qi + 1) * a.Lq;
+          if (whole) {
+            a.scores[qi * a.ss_n + (int64_t)b * a.ss_b] = sum;
+          } else {
+            a.partial[(int64_t)rb * a.Nq * a.B + qi * a.B + b] = sum;
+          }
+        }
+      }
+      par ^= 1;
+    }
+    if (!has_next) break;
+    if (nb_doc != b) {
+      b = nb_doc;
+      len = nlen;
+      nt = len > 0 ? (len + TJ - 1) / TJ : 1;
+      rd = rd_next;
+    }
+    t = nt_tile;
+    buf ^= 1;
+  }
+}
+
+// scores of queries that straddle row blocks: sum of their partial slots in
+// row-block order.
+__global__ void __launch_bounds__(256) tiled_sum_parts_kernel(FwdArgs a, int R) {
+  const int64_t items = (int64_t)a.Nq * a.B;
+  const int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= items) return;
+  const int64_t qi = item / a.B, b = item - qi * a.B;
+  const int64_t rb0 = qi * a.Lq / R, rb1 = ((qi + 1) * a.Lq - 1) / R;
+  if (rb0 == rb1) return;  // written directly by its row block
+  float s = 0.f;
+  for (int64_t rb = rb0; rb <= rb1; ++rb) s += a.partial[rb * items + item];
+  a.scores[qi * a.ss_n + b * a.ss_b] = s;
+}
+
+template <int KIND, int NB, int KS, bool KMASK, bool ARGMAX>
+hipError_t launch_one(const FwdArgs& a, const TiledPlan& p, hipStream_t s) {
+  hipLaunchKernelGGL((tiled_fwd_kernel<KIND, NB, KS, KMASK, ARGMAX>), dim3((unsigned)(p.nRB * p.G)), dim3(512), 0,
+                     s, a, p.nRB, p.G, p.xcd_map);
+  if (p.straddle) {
+    const int64_t items = (int64_t)a.Nq * a.B;
+    hipLaunchKernelGGL(tiled_sum_parts_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, a,
+                       p.rows_per_block);
+  }
+  return hipGetLastError();
+}
+
+template <int KIND, int NB, int KS>
+hipError_t dispatch_flags(const FwdArgs& a, const TiledPlan& p, bool am, hipStream_t s) {
+  const bool kmask = a.d != 32 * KS;
+  if (kmask) return am ? launch_one<KIND, NB, KS, true, true>(a, p, s) : launch_one<KIND, NB, KS, true, false>(a, p, s);
+  return am ? launch_one<KIND, NB, KS, false, true>(a, p, s) : launch_one<KIND, NB, KS, false, false>(a, p, s);
+}
+
+template <int KIND>
+hipError_t dispatch(const FwdArgs& a, const TiledPlan& p, bool am, hipStream_t s) {
+  if (p.ks == 4) {
+    if (p.nb == 8) return dispatch_flags<KIND, 8, 4>(a, p, am, s);
+    if (p.nb == 4) return dispatch_flags<KIND, 4, 4>(a, p, am, s);
+  } else if (p.ks == 8) {
+    if (p.nb == 4) return dispatch_flags<KIND, 4, 8>(a, p, am, s);
+    if (p.nb == 2) return dispatch_flags<KIND, 2, 8>(a, p, am, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+bool tiled_fwd_applicable(int64_t Nq, int64_t Lq, int d) { return d >= 1 && d <= 256 && Nq * Lq >= 256; }
+
+// Picks rows per wave (NB) and doc groups (G) for `cus` compute units, one
+// 8-wave workgroup per CU: minimise docs-per-workgroup x rows-per-block, the
+// MFMA time of the slowest workgroup; ties go to larger blocks (fewer re-reads
+// of each doc).
+TiledPlan tiled_fwd_plan(int64_t Nq, int64_t B, int64_t Lq, int d, int cus) {
+  TiledPlan best = {};
+  const int ks = d <= 128 ? 4 : 8;
+  const int nbs4[2] = {8, 4}, nbs8[2] = {4, 2};
+  const int* nbs = ks == 4 ? nbs4 : nbs8;
+  const int64_t rows = Nq * Lq;
+  double best_cost = 0;
+  for (int i = 0; i < 2; ++i) {
+    TiledPlan p = {};
+    p.ks = ks;
+    p.nb = nbs[i];
+    p.rows_per_block = kTiledWaves * 16 * p.nb;
+    p.nRB = (int)((rows + p.rows_per_block - 1) / p.rows_per_block);
+    int G = cus / p.nRB;
+    if (G < 1) G = 1;
+    if (G > B) G = (int)B;
+    p.xcd_map = 0;
+    if (G >= 8) {
+      G -= G % 8;
+      p.xcd_map = 1;
+    }
+    p.G = G;
+    const double cost = (double)((B + G - 1) / G) * (double)p.rows_per_block * (double)((p.nRB * G + cus - 1) / cus);
+    if (i == 0 || cost < best_cost) {
+      best = p;
+      best_cost = cost;
+    }
+  }
+  // queries straddling row blocks need the partial-sum pass
+  best.straddle = 0;
+  for (int64_t qi = 0; qi < Nq && !best.straddle; ++qi) {
+    if ((qi * Lq) / best.rows_per_block != ((qi + 1) * Lq - 1) / best.rows_per_block) best.straddle = 1;
+  }
+  return best;
+}
+
+size_t tiled_fwd_workspace_bytes(const TiledPlan& p, int64_t Nq, int64_t B) {
+  return p.straddle ? (size_t)p.nRB * (size_t)Nq * (size_t)B * sizeof(float) : 0;
+}
+
+hipError_t launch_tiled_fwd(int kind, const FwdArgs& a, const TiledPlan& p, bool with_argmax, hipStream_t s) {
+  switch (kind) {
+    case KIND_F16: return dispatch<KIND_F16>(a, p, with_argmax, s);
+    case KIND_BF16: return dispatch<KIND_BF16>(a, p, with_argmax, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace fmx

@@ -61,6 +61,23 @@ int splitd_fwd_nqb(int Lq, int d);    // 16-token query blocks per pass
 int splitd_fwd_passes(int Lq, int d); // > 1: partial sums in FwdArgs::partial
 hipError_t launch_splitd_fwd(int kind, const FwdArgs& a, bool with_argmax, hipStream_t s);
 
+// Tiled kernel (MFMA-bound regime): persistent 8-wave workgroups keep a block
+// of query rows in VGPRs and stream shared docs through LDS. d <= 256 and at
+// least 256 query rows in total.
+struct TiledPlan {
+  int ks;              // 32-wide k-steps (4: d <= 128, 8: d <= 256)
+  int nb;              // 16-row query blocks per wave
+  int rows_per_block;  // 8 * 16 * nb
+  int nRB;             // row blocks over the Nq*Lq flattened query rows
+  int G;               // doc groups (workgroups per row block)
+  int xcd_map;         // XCD-aware blockIdx mapping (G % 8 == 0)
+  int straddle;        // some query spans two row blocks: partial sums + second pass
+};
+bool tiled_fwd_applicable(int64_t Nq, int64_t Lq, int d);
+TiledPlan tiled_fwd_plan(int64_t Nq, int64_t B, int64_t Lq, int d, int cus);
+size_t tiled_fwd_workspace_bytes(const TiledPlan& p, int64_t Nq, int64_t B);
+hipError_t launch_tiled_fwd(int kind, const FwdArgs& a, const TiledPlan& p, bool with_argmax, hipStream_t s);
+
 // dQ / dD of the argmax backward.
 int bwd_dq_chunks(int B, int Lq, int d);
 size_t bwd_dd_lds_bytes(int Lq, int Ld);  // dynamic LDS of the dD kernel

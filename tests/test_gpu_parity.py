@@ -362,3 +362,37 @@ def test_maxsim_naive_on_gpu(oracle_mod):
     lengths = torch.tensor([60, 0, 1, 30, 59, 60, 10, 20, 40, 50], dtype=torch.int32)
     out = fm.maxsim_naive(Q.to(DEV), D.to(DEV), lengths.to(DEV))
     assert_scores(out, oracle_mod.maxsim(to_np32(Q), to_np32(D), lengths.numpy())[0], atol=1e-4)
+
+
+# ------------------------------------------------- tiled (many query rows) ----
+
+@pytest.mark.parametrize("Nq, Lq, B, Ld, d", [
+    (1, 256, 30, 100, 128),     # smallest row count routed to the tiled kernel
+    (1, 2048, 5, 70, 128),      # one query over two row blocks: partial sums
+    (3, 700, 9, 90, 128),       # queries straddling row-block boundaries
+    (40, 32, 37, 75, 128),      # batched, B not a multiple of the doc groups
+    (16, 32, 300, 64, 256),     # d = 256 (8 k-steps)
+    (8, 64, 20, 50, 200),       # d not a multiple of 32
+    (2, 300, 3, 1030, 96),      # long docs, few docs (fewer doc groups than CUs)
+])
+def test_tiled_shapes(oracle_mod, Nq, Lq, B, Ld, d):
+    Q = sim((Nq, Lq, d), 800 + Lq + d)
+    D = sim((B, Ld, d), 801 + B)
+    lengths = torch.randint(0, Ld + 20, (B,), generator=torch.Generator().manual_seed(B), dtype=torch.int32)
+    out = fm.flash_maxsim_batched(Q.to(DEV), D.to(DEV), lengths.to(DEV))
+    ref = oracle_mod.maxsim(to_np32(Q), to_np32(D), lengths.numpy())
+    assert_scores(out, ref)
+
+
+def test_tiled_bf16_and_argmax(oracle_mod):
+    s, dQ, dD, ref, am_ref, best, Qn, Dn, g = run_train(oracle_mod, 6, 512, 100, 128, 820, torch.bfloat16)
+    assert_scores(s, ref[0])
+    from flash_maxsim_amd.flash_maxsim import _launch_fwd, _prep
+
+    Q2 = _prep(torch.from_numpy(Qn).to(torch.bfloat16).to(DEV), torch.bfloat16)
+    D2 = _prep(torch.from_numpy(Dn).to(torch.bfloat16).to(DEV), torch.bfloat16)
+    _, am = _launch_fwd(Q2[None], D2, None, 1, 6, 512, 100, 128, True, True)
+    assert_argmax(am, am_ref, best, Qn, Dn, 128)
+    dQ_ref, dD_ref = oracle_mod.bwd(Qn, Dn, am.cpu().numpy(), g.numpy())
+    np.testing.assert_allclose(dQ.double().cpu().numpy(), dQ_ref, rtol=1e-2, atol=2e-2)
+    np.testing.assert_allclose(dD.double().cpu().numpy(), dD_ref, rtol=1e-2, atol=2e-2)
