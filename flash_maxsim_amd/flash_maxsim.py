@@ -99,65 +99,75 @@ def _launch_fwd(Q, D, lengths, Nq, B, Lq, Ld, d, shared_docs, save_argmax):
 
 
 def flash_maxsim(Q: torch.Tensor, D: torch.Tensor, doc_lengths=None) -> torch.Tensor:
-    """Compute MaxSim scores. Q: [Lq, d], D: [B, Ld, d] -> [B]."""
-    assert Q.dim() == 2 and D.dim() == 3 and Q.shape[1] == D.shape[2]
+    """Scores one query against every doc: float32 [B].
+
+    Q is [Lq, d], D is [B, Ld, d]; score[b] adds up, over the query tokens, the
+    best similarity among doc b's first doc_lengths[b] tokens (all Ld when
+    doc_lengths is None). Reference signature: flash_maxsim.py:221.
+    """
+    assert Q.ndim == 2 and D.ndim == 3 and Q.size(1) == D.size(2)
     Lq, d = Q.shape
-    B, Ld, _ = D.shape
-    dt = _kernel_dtype(Q, D)
-    Q2 = _prep(Q, dt)
-    D2 = _prep(D, dt)
+    B, Ld = D.shape[:2]
+    kdt = _kernel_dtype(Q, D)
     lengths = _lengths(B, D.device, doc_lengths)
-    scores, _ = _launch_fwd(Q2.unsqueeze(0), D2, lengths, 1, B, Lq, Ld, d, True, False)
-    return scores.squeeze(0)
+    scores, _ = _launch_fwd(_prep(Q, kdt).unsqueeze(0), _prep(D, kdt), lengths, 1, B, Lq, Ld, d, True, False)
+    return scores[0]
 
 
 def flash_maxsim_batched(Q: torch.Tensor, D: torch.Tensor, doc_lengths=None,
                          shared_docs: bool = True) -> torch.Tensor:
-    """Batched MaxSim. Q: [Nq, Lq, d], D: [B, Ld, d] -> [Nq, B]."""
-    assert Q.dim() == 3 and Q.shape[2] == D.shape[-1]
+    """Scores Nq queries at once: float32 [Nq, B].
+
+    Q is [Nq, Lq, d]. With shared_docs every query meets the same docs D
+    [B, Ld, d]; otherwise query i has its own docs D[i] of D [Nq, B, Ld, d] and
+    doc_lengths, if given, holds Nq*B entries in that order. Reference
+    signature: flash_maxsim.py:233.
+    """
+    assert Q.ndim == 3 and Q.size(2) == D.size(-1)
     Nq, Lq, d = Q.shape
     if shared_docs:
-        assert D.dim() == 3
-        B, Ld, _ = D.shape
+        assert D.ndim == 3
+        B, Ld = D.shape[:2]
+        doc_rows = D
     else:
-        assert D.dim() == 4 and D.shape[0] == Nq
-        _, B, Ld, _ = D.shape
-        D = D.reshape(Nq * B, Ld, d)
-    dt = _kernel_dtype(Q, D)
-    Q2 = _prep(Q, dt)
-    D2 = _prep(D, dt)
-    total = B if shared_docs else Nq * B
-    lengths = _lengths(total, D.device, doc_lengths)
-    scores, _ = _launch_fwd(Q2, D2, lengths, Nq, B, Lq, Ld, d, shared_docs, False)
+        assert D.ndim == 4 and D.size(0) == Nq
+        B, Ld = D.shape[1:3]
+        doc_rows = D.reshape(Nq * B, Ld, d)
+    kdt = _kernel_dtype(Q, doc_rows)
+    lengths = _lengths(doc_rows.size(0), D.device, doc_lengths)
+    scores, _ = _launch_fwd(_prep(Q, kdt), _prep(doc_rows, kdt), lengths, Nq, B, Lq, Ld, d, shared_docs, False)
     return scores
 
 
 class _FlashMaxSimFn(torch.autograd.Function):
-    """Forward saves per-(doc, query token) argmax; backward scatters through it
-    (reference flash_maxsim.py:253-286)."""
+    """Autograd node of flash_maxsim_train (reference flash_maxsim.py:253-286).
+
+    The forward kernel records, for every (doc, query token), the first doc
+    token reaching the max; the gradient of a max flows only to that token, so
+    the backward is a gather (dQ) and a scatter (dD) through those indices.
+    """
 
     @staticmethod
     def forward(ctx, Q, D):
         Lq, d = Q.shape
-        B, Ld, _ = D.shape
-        dt = _kernel_dtype(Q, D)
-        Q2 = _prep(Q, dt)
-        D2 = _prep(D, dt)
-        scores, argmax = _launch_fwd(Q2.unsqueeze(0), D2, None, 1, B, Lq, Ld, d, True, True)
-        ctx.save_for_backward(Q2, D2, argmax)
+        B, Ld = D.shape[:2]
+        kdt = _kernel_dtype(Q, D)
+        Qk, Dk = _prep(Q, kdt), _prep(D, kdt)
+        scores, argmax = _launch_fwd(Qk.unsqueeze(0), Dk, None, 1, B, Lq, Ld, d, True, True)
+        ctx.save_for_backward(Qk, Dk, argmax)
         ctx.d = d
-        return scores.squeeze(0)
+        return scores[0]
 
     @staticmethod
     def backward(ctx, grad_scores):
-        Q2, D2, argmax = ctx.saved_tensors
+        Qk, Dk, argmax = ctx.saved_tensors
         d = ctx.d
-        Lq = Q2.shape[0]
-        B, Ld, _ = D2.shape
+        Lq = Qk.shape[0]
+        B, Ld = Dk.shape[:2]
         need_q, need_d = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        dev = _check_devices(Q2, D2, grad_scores)
-        grad_Q = torch.empty(Lq, d, device=dev, dtype=Q2.dtype) if need_q else None
-        grad_D = torch.empty(B, Ld, d, device=dev, dtype=D2.dtype) if need_d else None
+        dev = _check_devices(Qk, Dk, grad_scores)
+        grad_Q = torch.empty(Lq, d, device=dev, dtype=Qk.dtype) if need_q else None
+        grad_D = torch.empty(B, Ld, d, device=dev, dtype=Dk.dtype) if need_d else None
         if (grad_Q is None and grad_D is None) or Lq == 0:
             if grad_Q is not None:
                 grad_Q.zero_()
@@ -170,26 +180,32 @@ class _FlashMaxSimFn(torch.autograd.Function):
         ws = _lib.workspace(nbytes, dev)
         with _device_guard(dev):
             rc = lib.fmx_bwd(
-                _lib.dtype_code(Q2), Q2.data_ptr(), Q2.stride(0), D2.data_ptr(), D2.stride(0), D2.stride(1),
+                _lib.dtype_code(Qk), Qk.data_ptr(), Qk.stride(0), Dk.data_ptr(), Dk.stride(0), Dk.stride(1),
                 argmax.data_ptr(), g.data_ptr(), _lib.ptr(grad_Q), _lib.ptr(grad_D),
-                B, Lq, Ld, d, _lib.ptr(ws), nbytes, _lib.stream_of(Q2),
+                B, Lq, Ld, d, _lib.ptr(ws), nbytes, _lib.stream_of(Qk),
             )
         _lib.check(rc)
         return grad_Q, grad_D
 
 
 def flash_maxsim_train(Q: torch.Tensor, D: torch.Tensor) -> torch.Tensor:
-    """MaxSim with autograd backward. Q: [Lq, d], D: [B, Ld, d] -> [B]."""
-    assert Q.dim() == 2 and D.dim() == 3 and Q.shape[1] == D.shape[2]
+    """flash_maxsim over full-length docs, differentiable in Q and D: float32 [B].
+
+    Gradients come back in the kernel dtype (fp16, or bf16 for bf16 inputs);
+    autograd casts them to the leaves' dtypes. Reference signature:
+    flash_maxsim.py:289.
+    """
+    assert Q.ndim == 2 and D.ndim == 3 and Q.size(1) == D.size(2)
     return _FlashMaxSimFn.apply(Q, D)
 
 
 def maxsim_naive(Q: torch.Tensor, D: torch.Tensor, doc_lengths=None) -> torch.Tensor:
-    """Reference PyTorch MaxSim. Q: [Lq, d], D: [B, Ld, d] -> [B].
+    """Unfused float32 MaxSim in plain torch, for checking: [B].
 
-    Plain torch in fp32 (reference flash_maxsim.py:294-301): S = D Q^T, tokens
-    at or past doc_lengths masked to -inf, max over doc tokens, sum over query
-    tokens. Runs wherever its inputs live.
+    Materialises every similarity, S = D Q^T per doc, masks doc tokens at or
+    past doc_lengths to -inf, takes the max over doc tokens and sums over
+    query tokens (reference flash_maxsim.py:294-301). Runs wherever its inputs
+    live, CPU included.
     """
     S = torch.matmul(D.float(), Q.float().t().contiguous())  # [B, Ld, Lq]
     if doc_lengths is not None:

@@ -19,28 +19,27 @@ from .flash_maxsim import _check_devices, _device_guard, _lengths, _prep
 
 
 def quantize_int8(D: torch.Tensor):
-    """Per-token affine INT8 quantization.
+    """Encodes every doc token as 8-bit codes on its own affine grid.
 
-    Args:
-        D: [B, Ld, d] float/half tensor.
-
-    Returns:
-        D_uint8: [B, Ld, d] uint8
-        scales:  [B, Ld, 1] float16
-        mins:    [B, Ld, 1] float16
+    For the d values x of one token, lo = min(x), step = max((max(x) - lo) / 255,
+    1e-8) in float32, and code = clamp(round_half_even((x - lo) / step), 0, 255).
+    Returns (codes uint8 [B, Ld, d], step fp16 [B, Ld, 1], lo fp16 [B, Ld, 1]):
+    codes come from the float32 step, the stored step and lo are rounded to
+    fp16 - the storage format flash_maxsim_int8 reads (reference
+    flash_maxsim_quant.py:11-28, whose arithmetic this matches bit for bit).
     """
     assert D.dim() == 3
-    Df = D.float()
-    d_min = Df.min(dim=-1, keepdim=True).values
-    d_max = Df.max(dim=-1, keepdim=True).values
-    scales = ((d_max - d_min) / 255.0).clamp_min(1e-8)
-    D_uint8 = ((Df - d_min) / scales).round().clamp(0, 255).to(torch.uint8)
-    return D_uint8, scales.half(), d_min.half()
+    x = D.to(torch.float32)
+    lo, hi = torch.aminmax(x, dim=-1, keepdim=True)
+    step = torch.clamp_min((hi - lo) / 255.0, 1e-8)
+    codes = torch.clamp(torch.round((x - lo) / step), 0, 255).to(torch.uint8)
+    return codes, step.to(torch.float16), lo.to(torch.float16)
 
 
 def dequantize_int8(D_uint8: torch.Tensor, scales: torch.Tensor, mins: torch.Tensor) -> torch.Tensor:
-    """Reconstruct float tensors from per-token affine INT8 encoding."""
-    return D_uint8.float() * scales.float() + mins.float()
+    """float32 doc tokens back from codes: code * step + lo (reference
+    flash_maxsim_quant.py:31-33; a separate multiply and add, no fma)."""
+    return D_uint8.to(torch.float32) * scales.to(torch.float32) + mins.to(torch.float32)
 
 
 def flash_maxsim_int8(
@@ -50,7 +49,12 @@ def flash_maxsim_int8(
     mins: torch.Tensor,
     doc_lengths=None,
 ) -> torch.Tensor:
-    """Fused dequant+MaxSim. Q: [Lq, d], D_uint8: [B, Ld, d] -> [B]."""
+    """flash_maxsim over quantize_int8-encoded docs: float32 [B].
+
+    Q is [Lq, d]; D_uint8 [B, Ld, d] uint8 codes with per-token scales and mins
+    of shape [B, Ld, 1] or [B, Ld]. Reference signature:
+    flash_maxsim_quant.py:105.
+    """
     assert Q.dim() == 2 and D_uint8.dim() == 3 and Q.shape[1] == D_uint8.shape[2]
     Lq, d = Q.shape
     B, Ld, _ = D_uint8.shape

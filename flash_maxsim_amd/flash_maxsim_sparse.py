@@ -20,16 +20,11 @@ def flash_maxsim_sparse(
     indices: torch.Tensor,
     doc_lengths=None,
 ) -> torch.Tensor:
-    """Sparse MaxSim with per-doc query token selection.
+    """flash_maxsim where doc b only sees K chosen query tokens: float32 [B].
 
-    Args:
-        Q: [Lq, d] query embeddings (shared across all docs)
-        D: [B, Ld, d] document embeddings
-        indices: [B, K] int — which query tokens to use per doc (same K for all)
-        doc_lengths: optional [B] int — variable doc lengths
-
-    Returns:
-        scores: [B] float32
+    Q is [Lq, d], D [B, Ld, d], indices [B, K] integer rows of Q for each doc
+    (a row outside [0, Lq) contributes a zero query token), doc_lengths
+    optional [B]. Reference signature: flash_maxsim_sparse.py:98.
     """
     assert Q.dim() == 2 and D.dim() == 3 and indices.dim() == 2
     Lq, d = Q.shape
@@ -68,11 +63,8 @@ def maxsim_sparse_naive(
     D: torch.Tensor,
     indices: torch.Tensor,
 ) -> torch.Tensor:
-    """Reference: sparse MaxSim with index buffer.
-
-    Args:
-        Q: [Lq, d], D: [B, Ld, d], indices: [B, K] int -> [B]
-    """
+    """Unfused float32 counterpart of flash_maxsim_sparse, for checking: [B]
+    (reference flash_maxsim_sparse.py:143-157; indices must be valid rows)."""
     Q_sel = Q[indices.long()].float()  # [B, K, d]
     S = torch.matmul(Q_sel, D.float().transpose(1, 2).contiguous())  # [B, K, Ld]
     return S.max(dim=2).values.sum(dim=1)
