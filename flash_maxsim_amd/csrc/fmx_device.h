@@ -2,7 +2,8 @@
 // (CDNA4, wave64): operand vector types, raw buffer resources, the fp16/bf16
 // MFMA wrapper, exact uint8 -> fp16 code conversion and wave reductions.
 //
-// Fragment convention used throughout (v_mfma_f32_16x16x32_{f16,bf16}):
+// Fragment convention of the 16x16x32 form (v_mfma_f32_16x16x32_{f16,bf16}),
+// used by the streaming and split-d kernels:
 //   lane l = 16*g + c   (c = l % 16, g = l / 16)
 //   A operand (16 x 32, M x K): lane l holds row c, k = 8*g .. 8*g+7
 //   B operand (32 x 16, K x N): lane l holds col c, k = 8*g .. 8*g+7
@@ -10,6 +11,12 @@
 // A k-step t of a d-wide row therefore covers k = 32*t + 8*g .. +7 for lane l.
 // Any permutation of k applied identically to A and B leaves A*B unchanged, so
 // both operands are loaded with the same (row, 32*t + 8*g) addressing.
+//
+// The 32x32x16 form (v_mfma_f32_32x32x16_{f16,bf16}), used by the tiled
+// kernel: lane l = 32*g + c (c = l % 32, g = l / 32) holds row (A) / column
+// (B) c and 8 k values; result register v of lane l is row 8*(v/4) + 4*g + v%4
+// of column c. On gfx950 this form retires twice the flops per cycle of the
+// 16x16x32 form, which is what the MFMA-bound shapes need.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -20,6 +27,7 @@ namespace fmx {
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
@@ -67,6 +75,22 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c)
                                                   __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
   }
 }
+
+// 32x32x16 MFMA, fp32 accumulate.
+template <bool BF>
+__device__ __forceinline__ f32x16_t mfma32x32x16(u32x4_t a, u32x4_t b, f32x16_t c) {
+  if constexpr (BF) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+}
+
+// IEEE maximum (NaN-propagating, as torch.max): v_maximum3_f32 on gfx950, with
+// no canonicalisation of MFMA results in front of it.
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
 // Eight uint8 codes -> eight fp16 values equal to the codes, exactly.
 // v_perm places code byte c under exponent byte 0x64, giving the fp16 value

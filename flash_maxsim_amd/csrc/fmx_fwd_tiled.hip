@@ -20,16 +20,24 @@
 // a query inside the row block is written to scores, a query straddling row
 // blocks to a partial slot that a second kernel adds in row-block order.
 //
-// blockIdx -> (row block, doc group) is XCD-aware when G % 8 == 0: the eight
-// XCDs take workgroups round-robin, so all row blocks of doc group g are put on
-// XCD g % 8 and read each doc tile through the same L2.
+// blockIdx -> (row block, doc group) is XCD-aware when the plan says so: the
+// eight XCDs take workgroups round-robin, so all row blocks of doc group g are
+// put on XCD g % 8 and read each doc tile through the same L2.
+//
+// The 16x16x32 MFMA form is used on purpose. The 32x32x16 form retires twice
+// the flops per instruction, but its 16-register results have to be folded out
+// of accumulation registers, and at the register budget of two waves per SIMD
+// a wave can then hold only half the query rows, doubling the LDS reads per
+// flop. On random data, where the GPU runs power-limited, this layout measured
+// faster (config 2: 182 us, against 218-275 us for 32x32x16 variants).
 #include "fmx_kernels.h"
 #include "fmx_tile.h"
 
 namespace fmx {
 namespace {
 
-constexpr int kTiledWaves = 8;
+constexpr int kTiledNW = 8;                  // waves per workgroup (one workgroup per CU,
+constexpr int kTiledWPC = 8 / kTiledNW;      // two waves per SIMD)
 constexpr int kTileTokens = 64;
 
 // A-fragments of 16-token subtile s from an LDS tile with ROWB-byte rows.
@@ -71,13 +79,14 @@ __device__ __forceinline__ void fold_rows(f32x4_t acc, int rowj, int len, bool t
       }
     }
   } else {
-    m = fmaxf(m, fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3])));
+    m = vmax(m, vmax(vmax(acc[0], acc[1]), vmax(acc[2], acc[3])));
   }
 }
 
-template <int KIND, int NB, int KS, bool KMASK, bool ARGMAX>
-__global__ void __launch_bounds__(512) tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
-  constexpr int NW = kTiledWaves, TJ = kTileTokens;
+template <int KIND, int NW, int NB, int KS, bool KMASK, bool ARGMAX>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
+  constexpr int TJ = kTileTokens;
   constexpr int ROWB = 64 * KS + 16;       // LDS bytes per token row (16 B pad)
   constexpr int BUFB = TJ * ROWB;          // LDS bytes per tile buffer
   constexpr int CPR = 4 * KS;              // 16-byte chunks per token row
@@ -242,7 +251,7 @@ __global__ void __launch_bounds__(512) tiled_fwd_kernel(FwdArgs a, int nRB, int 
             const int oi = __shfl_xor(ix, sh);
             argmax_merge(v, ix, ov, oi);
           } else {
-            v = fmaxf(v, ov);
+            v = vmax(v, ov);
           }
         }
         if (g == 0) {
@@ -305,9 +314,9 @@ __global__ void __launch_bounds__(256) tiled_sum_parts_kernel(FwdArgs a, int R) 
   a.scores[qi * a.ss_n + b * a.ss_b] = s;
 }
 
-template <int KIND, int NB, int KS, bool KMASK, bool ARGMAX>
+template <int KIND, int NW, int NB, int KS, bool KMASK, bool ARGMAX>
 hipError_t launch_one(const FwdArgs& a, const TiledPlan& p, hipStream_t s) {
-  hipLaunchKernelGGL((tiled_fwd_kernel<KIND, NB, KS, KMASK, ARGMAX>), dim3((unsigned)(p.nRB * p.G)), dim3(512), 0,
+  hipLaunchKernelGGL((tiled_fwd_kernel<KIND, NW, NB, KS, KMASK, ARGMAX>), dim3((unsigned)p.grid), dim3(NW * 64), 0,
                      s, a, p.nRB, p.G, p.xcd_map);
   if (p.straddle) {
     const int64_t items = (int64_t)a.Nq * a.B;
@@ -317,21 +326,23 @@ hipError_t launch_one(const FwdArgs& a, const TiledPlan& p, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int KIND, int NB, int KS>
+template <int KIND, int NW, int NB, int KS>
 hipError_t dispatch_flags(const FwdArgs& a, const TiledPlan& p, bool am, hipStream_t s) {
   const bool kmask = a.d != 32 * KS;
-  if (kmask) return am ? launch_one<KIND, NB, KS, true, true>(a, p, s) : launch_one<KIND, NB, KS, true, false>(a, p, s);
-  return am ? launch_one<KIND, NB, KS, false, true>(a, p, s) : launch_one<KIND, NB, KS, false, false>(a, p, s);
+  if (kmask) {
+    return am ? launch_one<KIND, NW, NB, KS, true, true>(a, p, s) : launch_one<KIND, NW, NB, KS, true, false>(a, p, s);
+  }
+  return am ? launch_one<KIND, NW, NB, KS, false, true>(a, p, s) : launch_one<KIND, NW, NB, KS, false, false>(a, p, s);
 }
 
 template <int KIND>
 hipError_t dispatch(const FwdArgs& a, const TiledPlan& p, bool am, hipStream_t s) {
   if (p.ks == 4) {
-    if (p.nb == 8) return dispatch_flags<KIND, 8, 4>(a, p, am, s);
-    if (p.nb == 4) return dispatch_flags<KIND, 4, 4>(a, p, am, s);
+    if (p.nb == 8) return dispatch_flags<KIND, kTiledNW, 8, 4>(a, p, am, s);
+    if (p.nb == 4) return dispatch_flags<KIND, kTiledNW, 4, 4>(a, p, am, s);
   } else if (p.ks == 8) {
-    if (p.nb == 4) return dispatch_flags<KIND, 4, 8>(a, p, am, s);
-    if (p.nb == 2) return dispatch_flags<KIND, 2, 8>(a, p, am, s);
+    if (p.nb == 4) return dispatch_flags<KIND, kTiledNW, 4, 8>(a, p, am, s);
+    if (p.nb == 2) return dispatch_flags<KIND, kTiledNW, 2, 8>(a, p, am, s);
   }
   return hipErrorInvalidValue;
 }
@@ -340,36 +351,51 @@ hipError_t dispatch(const FwdArgs& a, const TiledPlan& p, bool am, hipStream_t s
 
 bool tiled_fwd_applicable(int64_t Nq, int64_t Lq, int d) { return d >= 1 && d <= 256 && Nq * Lq >= 256; }
 
-// Picks rows per wave (NB) and doc groups (G) for `cus` compute units, one
-// 8-wave workgroup per CU: minimise docs-per-workgroup x rows-per-block, the
-// MFMA time of the slowest workgroup; ties go to larger blocks (fewer re-reads
-// of each doc).
+// Picks rows per wave (NB) and doc groups (G). `slots` workgroups run at once
+// (kTiledWPC per CU, two waves per SIMD). The slowest workgroup's MFMA time is
+// proportional to docs-per-group x rows-per-block. The XCD-aware mapping puts
+// all row blocks of a doc group on one XCD (G a multiple of 8, nRB * G / 8
+// workgroups per XCD), so each doc tile is fetched once per XCD L2; without
+// it the row blocks of a doc meet in the shared last-level cache instead,
+// which is counted as a few percent of extra cost.
 TiledPlan tiled_fwd_plan(int64_t Nq, int64_t B, int64_t Lq, int d, int cus) {
   TiledPlan best = {};
   const int ks = d <= 128 ? 4 : 8;
   const int nbs4[2] = {8, 4}, nbs8[2] = {4, 2};
   const int* nbs = ks == 4 ? nbs4 : nbs8;
+  const int slots = (cus > 0 ? cus : 256) * kTiledWPC;
+  const int per_xcd = slots / 8;
   const int64_t rows = Nq * Lq;
   double best_cost = 0;
+  bool have = false;
   for (int i = 0; i < 2; ++i) {
-    TiledPlan p = {};
-    p.ks = ks;
-    p.nb = nbs[i];
-    p.rows_per_block = kTiledWaves * 16 * p.nb;
-    p.nRB = (int)((rows + p.rows_per_block - 1) / p.rows_per_block);
-    int G = cus / p.nRB;
-    if (G < 1) G = 1;
-    if (G > B) G = (int)B;
-    p.xcd_map = 0;
-    if (G >= 8) {
-      G -= G % 8;
-      p.xcd_map = 1;
-    }
-    p.G = G;
-    const double cost = (double)((B + G - 1) / G) * (double)p.rows_per_block * (double)((p.nRB * G + cus - 1) / cus);
-    if (i == 0 || cost < best_cost) {
-      best = p;
-      best_cost = cost;
+    for (int xcd = 1; xcd >= 0; --xcd) {
+      TiledPlan p = {};
+      p.ks = ks;
+      p.nb = nbs[i];
+      p.rows_per_block = kTiledNW * 16 * p.nb;
+      p.nRB = (int)((rows + p.rows_per_block - 1) / p.rows_per_block);
+      int G;
+      if (xcd) {
+        if (p.nRB > per_xcd || B < 8) continue;
+        G = 8 * (per_xcd / p.nRB);
+        if (G > B) G = (int)(B - B % 8);
+        p.grid = 8 * p.nRB * (G / 8);
+      } else {
+        G = slots / p.nRB;
+        if (G < 1) G = 1;
+        if (G > B) G = (int)B;
+        p.grid = p.nRB * G;
+      }
+      p.xcd_map = xcd;
+      p.G = G;
+      const double rounds = (double)(((int64_t)p.grid + slots - 1) / slots);
+      const double cost = (double)((B + G - 1) / G) * (double)p.rows_per_block * rounds * (xcd ? 1.0 : 1.04);
+      if (!have || cost < best_cost) {
+        best = p;
+        best_cost = cost;
+        have = true;
+      }
     }
   }
   // queries straddling row blocks need the partial-sum pass

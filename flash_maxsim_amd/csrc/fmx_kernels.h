@@ -71,6 +71,7 @@ struct TiledPlan {
   int nRB;             // row blocks over the Nq*Lq flattened query rows
   int G;               // doc groups (workgroups per row block)
   int xcd_map;         // XCD-aware blockIdx mapping (G % 8 == 0)
+  int grid;            // workgroups launched
   int straddle;        // some query spans two row blocks: partial sums + second pass
 };
 bool tiled_fwd_applicable(int64_t Nq, int64_t Lq, int d);
