@@ -224,12 +224,13 @@ int fmx_fwd_int8(const void* Q, int64_t q_stride_l, const uint8_t* D, int64_t d_
   a.Ld = (int)Ld;
   a.d = (int)d;
   a.shared_docs = 1;
-  // Four scales per 8-byte load needs 8-byte aligned doc rows of scales and a
-  // padded length that never passes the end of a doc's row.
-  a.sm_vec = ((sm_stride_b & 3) == 0 && (Ld & 3) == 0 &&
-              ((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(mins)) & 7u) == 0)
-                 ? 1
-                 : 0;
+  // The vector path reads codes 16 bytes at a time (16-byte aligned rows) and
+  // four scales per 8-byte load, which needs 8-byte aligned doc rows of scales
+  // and a padded length that never passes the end of a doc's row.
+  a.vec = ((d_stride_b & 15) == 0 && (d_stride_l & 15) == 0 && (sm_stride_b & 3) == 0 && (Ld & 3) == 0 &&
+           ((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(mins)) & 7u) == 0)
+              ? 1
+              : 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const hipError_t e = plan_fwd(Lq, d).splitd ? fmx::launch_splitd_fwd(fmx::KIND_U8, a, false, s)
                                               : fmx::launch_stream_fwd(fmx::KIND_U8, a, false, s);

@@ -92,21 +92,25 @@ __device__ __forceinline__ f32x16_t mfma32x32x16(u32x4_t a, u32x4_t b, f32x16_t 
 // no canonicalisation of MFMA results in front of it.
 __device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
-// Eight uint8 codes -> eight fp16 values equal to the codes, exactly.
-// v_perm places code byte c under exponent byte 0x64, giving the fp16 value
-// 1024 + c (exact: 1024 + c < 2048 has an 11-bit significand); one packed fp16
-// subtraction of 1024 then leaves c exactly.
-__device__ __forceinline__ u32x4_t codes_to_f16(u32x2_t raw) {
+// Eight uint8 codes -> eight fp16 values 1024 + code, exactly: v_perm places
+// code byte c under exponent byte 0x64, which is the fp16 value 1024 + c
+// (1024 + c < 2048 fits the 11-bit significand). The uint8 kernels multiply
+// these biased values on the MFMA and remove the bias in the per-token affine
+// epilogue: Q . (1024 + c) = Q . c + 1024 * sum(Q), so with the stored
+// (scale, min) of a token, Q . (scale * c + min) = scale * Q . (1024 + c) +
+// (min - 1024 * scale) * sum(Q). Four VALU ops per 8 codes, no fp16 subtract.
+__device__ __forceinline__ u32x4_t codes_to_f16_biased(u32x2_t raw) {
   const uint32_t hi = 0x64646464u;
   u32x4_t h;
   h[0] = __builtin_amdgcn_perm(hi, raw[0], 0x04010400u);
   h[1] = __builtin_amdgcn_perm(hi, raw[0], 0x04030402u);
   h[2] = __builtin_amdgcn_perm(hi, raw[1], 0x04010400u);
   h[3] = __builtin_amdgcn_perm(hi, raw[1], 0x04030402u);
-  f16x8_t v = __builtin_bit_cast(f16x8_t, h);
-  v = v - (f16x8_t)((_Float16)1024.0f);
-  return __builtin_bit_cast(u32x4_t, v);
+  return h;
 }
+
+// Bias of codes_to_f16_biased.
+constexpr float kCodeBias = 1024.0f;
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);

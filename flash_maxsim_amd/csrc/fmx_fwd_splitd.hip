@@ -22,7 +22,8 @@ namespace {
 
 constexpr int kSplitWaves = 8;
 
-template <int KIND, int NQB, int KSW, bool KMASK, bool ARGMAX>
+// VEC: uint8 vector load path (FwdArgs::vec); true for fp16/bf16.
+template <int KIND, int NQB, int KSW, bool KMASK, bool ARGMAX, bool VEC>
 __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
   constexpr int NW = kSplitWaves, QROWS = NQB * 16;
   constexpr int P = KSW >= 8 ? 2 : 3;  // tiles in flight per wave
@@ -54,10 +55,12 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
   const int ntiles = (len + 15) >> 4;
   const bool owner = wave < NQB;  // wave w reduces and maxes query block w
 
-  const int tbase = wave * KSW;  // first global k-step of this wave
+  const int tbase = wave * KSW;  // first global k-step of this wave (KSW is even)
   const int kp = a.d & ~7;
-  const int tp = (kp >> 5) - tbase;  // local k-step of the partial group, if any
-  const u32x4_t pmask = prefix_mask16(g == ((kp >> 3) & 3) ? (a.d & 7) : 8);
+  int tp, gp;  // local slot of the partial group (out of range: another wave's)
+  frag_slot<KIND>(kp - 32 * tbase, tp, gp);
+  if (kp < 32 * tbase) tp = -1;
+  const u32x4_t pmask = prefix_mask16(g == gp ? (a.d & 7) : 8);
   const bool has_partial = KMASK && (a.d & 7) != 0;
 
   // ---- query slice of this pass ----
@@ -69,7 +72,7 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
     const uint32_t rowoff = query_row_offset(a, b, q0 + nb * 16 + c);
 #pragma unroll
     for (int t = 0; t < KSW; ++t) {
-      const int k0 = 32 * (tbase + t) + 8 * g;
+      const int k0 = 32 * tbase + frag_k0<KIND>(t, g);
       if constexpr (KMASK) {
         qf[nb][t] = ld16(rq, k0 < a.d ? rowoff + (uint32_t)(k0 * 2) : kOOB);
         if (has_partial && t == tp) qf[nb][t] &= pmask;
@@ -97,11 +100,11 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
   }
 
   // ---- doc stream ----
-  const DocRes dr = make_doc_res<KIND>(a.D, drow, a.sd_b, a.sd_l, len, a.scales, a.mins, a.sm_b, a.sm_vec);
+  const DocRes dr = make_doc_res<KIND, VEC>(a.D, drow, a.sd_b, a.sd_l, len, a.scales, a.mins, a.sm_b);
   uint32_t koff[KSW];
 #pragma unroll
   for (int t = 0; t < KSW; ++t) {
-    const int k0 = 32 * (tbase + t) + 8 * g;
+    const int k0 = 32 * tbase + frag_k0<KIND>(t, g);
     koff[t] = (KMASK && k0 >= a.d) ? kOOB : (uint32_t)(k0 * ESZ);  // past d: zeros
   }
 
@@ -110,12 +113,12 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
   Tile<KIND, KSW> buf[P];
 #pragma unroll
   for (int s = 0; s < P; ++s)
-    if (s < ntiles) load_tile<KIND, KSW>(buf[s], dr, s, c, g, koff);
+    if (s < ntiles) load_tile<KIND, KSW, VEC>(buf[s], dr, s, c, g, koff);
   for (int i0 = 0; i0 < ntiles; i0 += P) {
 #pragma unroll
     for (int s = 0; s < P; ++s) {
       const int tile = i0 + s;
-      if (tile < ntiles) {
+      if (tile < ntiles) {  // uniform over the workgroup: the barriers below are safe
         u32x4_t af[KSW];
 #pragma unroll
         for (int t = 0; t < KSW; ++t) {
@@ -124,16 +127,12 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
             if (has_partial && t == tp) af[t] &= pmask;
           }
         }
-        float sc[4], mn[4];
+        float sc[4], off[4];
         if constexpr (U8) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            sc[r] = tile_scale(buf[s].s, r);
-            mn[r] = tile_scale(buf[s].m, r);
-          }
+          for (int r = 0; r < 4; ++r) tile_affine(buf[s].s, buf[s].m, r, sc[r], off[r]);
         }
-        if (tile + P < ntiles) load_tile<KIND, KSW>(buf[s], dr, tile + P, c, g, koff);
-
+        if (tile + P < ntiles) load_tile<KIND, KSW, VEC>(buf[s], dr, tile + P, c, g, koff);
 #pragma unroll
         for (int nb = 0; nb < NQB; ++nb) {
           f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -148,7 +147,7 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
           for (int w = 1; w < NW; ++w) S += part[w][wave][lane];
           if constexpr (U8) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) S[r] = fmaf(sc[r], S[r], mn[r] * qsum);
+            for (int r = 0; r < 4; ++r) S[r] = fmaf(sc[r], S[r], off[r] * qsum);
           }
           const int row0 = tile * 16 + 4 * g;
           if (tile * 16 + 16 > len) {
@@ -165,7 +164,7 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
               }
             }
           } else {
-            m = fmaxf(m, fmaxf(fmaxf(S[0], S[1]), fmaxf(S[2], S[3])));
+            m = vmax(m, vmax(vmax(S[0], S[1]), vmax(S[2], S[3])));
           }
         }
         __syncthreads();
@@ -184,7 +183,7 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
         const int oi = __shfl_xor(ix, s);
         argmax_merge(v, ix, ov, oi);
       } else {
-        v = fmaxf(v, ov);
+        v = vmax(v, ov);
       }
     }
     if (g == 0) {
@@ -223,12 +222,12 @@ __global__ void __launch_bounds__(256) splitd_sum_passes_kernel(FwdArgs a, int n
   a.scores[qi * a.ss_n + b * a.ss_b] = s;
 }
 
-template <int KIND, int NQB, int KSW, bool KMASK, bool ARGMAX>
+template <int KIND, int NQB, int KSW, bool KMASK, bool ARGMAX, bool VEC = true>
 hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
   constexpr int QROWS = NQB * 16;
   const int npass = (a.Lq + QROWS - 1) / QROWS;
   const int64_t items = (int64_t)a.Nq * a.B;
-  hipLaunchKernelGGL((splitd_fwd_kernel<KIND, NQB, KSW, KMASK, ARGMAX>), dim3((unsigned)items, npass),
+  hipLaunchKernelGGL((splitd_fwd_kernel<KIND, NQB, KSW, KMASK, ARGMAX, VEC>), dim3((unsigned)items, npass),
                      dim3(512), 0, s, a);
   if (npass > 1) {
     hipLaunchKernelGGL(splitd_sum_passes_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, a,
@@ -242,7 +241,12 @@ hipError_t dispatch_flags(const FwdArgs& a, bool am, hipStream_t s) {
   const bool kmask = a.d != 32 * KSW * kSplitWaves;
   if constexpr (KIND == KIND_U8) {
     (void)am;
-    return kmask ? launch_one<KIND, NQB, KSW, true, false>(a, s) : launch_one<KIND, NQB, KSW, false, false>(a, s);
+    if (a.vec) {
+      return kmask ? launch_one<KIND, NQB, KSW, true, false, true>(a, s)
+                   : launch_one<KIND, NQB, KSW, false, false, true>(a, s);
+    }
+    return kmask ? launch_one<KIND, NQB, KSW, true, false, false>(a, s)
+                 : launch_one<KIND, NQB, KSW, false, false, false>(a, s);
   } else {
     if (kmask) return am ? launch_one<KIND, NQB, KSW, true, true>(a, s) : launch_one<KIND, NQB, KSW, true, false>(a, s);
     return am ? launch_one<KIND, NQB, KSW, false, true>(a, s) : launch_one<KIND, NQB, KSW, false, false>(a, s);

@@ -16,8 +16,10 @@
 //    (plus the first index reaching it, when argmax is requested);
 //  * at the end lanes merge across row groups with cross-lane shuffles, waves
 //    merge through LDS, and wave 0 sums over query tokens into one fp32 score.
-// uint8 docs use S = scale_j * (Q . codes_j) + min_j * sum_k Q_k with the
-// codes widened to fp16 exactly, which equals Q . dequantize(codes) in fp32.
+// uint8 docs use S = scale_j * (Q . (1024 + codes_j)) + (min_j - 1024 * scale_j)
+// * sum_k Q_k, with the codes widened to the fp16 values 1024 + code exactly
+// (one v_perm per two codes); this equals Q . dequantize(codes) up to fp32
+// rounding.
 // Queries longer than 16*NQB tokens run as blockIdx.y passes whose partial sums
 // a second kernel adds in pass order.
 #include "fmx_kernels.h"
@@ -27,12 +29,17 @@ namespace fmx {
 namespace {
 
 constexpr int kStreamWaves = 4;
-constexpr int kStreamDepth = 4;  // tiles in flight per wave
+// Tiles in flight per wave. Deeper uint8 rings (half the bytes per tile) cost
+// the third wave per SIMD, which hides more of the per-tile dequant work than
+// the extra bytes in flight gain.
+template <int KIND>
+constexpr int stream_depth() { return 4; }
 
 // KMASK: d is not exactly 32*KS, so fragment slots past d must read as zero.
-template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX>
+// VEC: uint8 vector load path (FwdArgs::vec); true for fp16/bf16.
+template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX, bool VEC>
 __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
-  constexpr int NW = kStreamWaves, P = kStreamDepth, QROWS = NQB * 16;
+  constexpr int NW = kStreamWaves, P = stream_depth<KIND>(), QROWS = NQB * 16;
   constexpr int ESZ = KindInfo<KIND>::esz;
   constexpr bool BF = KindInfo<KIND>::bf;
   constexpr bool U8 = KIND == KIND_U8;
@@ -62,8 +69,9 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
 
   // Partial 8-wide group (d % 8 != 0): fragment slot tp of lane group gp.
   const int kp = a.d & ~7;
-  const int tp = kp >> 5;
-  const u32x4_t pmask = prefix_mask16(g == ((kp >> 3) & 3) ? (a.d & 7) : 8);
+  int tp, gp;
+  frag_slot<KIND>(kp, tp, gp);
+  const u32x4_t pmask = prefix_mask16(g == gp ? (a.d & 7) : 8);
   const bool has_partial = KMASK && (a.d & 7) != 0;
 
   // ---- query tile of this pass (B operand) ----
@@ -76,7 +84,7 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
     const uint32_t rowoff = query_row_offset(a, b, q0 + nb * 16 + c);
 #pragma unroll
     for (int t = 0; t < KS; ++t) {
-      const int k0 = 32 * t + 8 * g;
+      const int k0 = frag_k0<KIND>(t, g);
       if constexpr (KMASK) {
         qf[nb][t] = ld16(rq, k0 < a.d ? rowoff + (uint32_t)(k0 * 2) : kOOB);
         if (has_partial && t == tp) qf[nb][t] &= pmask;
@@ -96,11 +104,11 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
   }
 
   // ---- doc stream ----
-  const DocRes dr = make_doc_res<KIND>(a.D, drow, a.sd_b, a.sd_l, len, a.scales, a.mins, a.sm_b, a.sm_vec);
+  const DocRes dr = make_doc_res<KIND, VEC>(a.D, drow, a.sd_b, a.sd_l, len, a.scales, a.mins, a.sm_b);
   uint32_t koff[KS];
 #pragma unroll
   for (int t = 0; t < KS; ++t) {
-    const int k0 = 32 * t + 8 * g;
+    const int k0 = frag_k0<KIND>(t, g);
     // Slots past d read as zeros instead of touching the next row.
     koff[t] = (KMASK && k0 >= a.d) ? kOOB : (uint32_t)(k0 * ESZ);
   }
@@ -116,7 +124,7 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
   Tile<KIND, KS> buf[P];
 #pragma unroll
   for (int s = 0; s < P; ++s)
-    if (s < my_n) load_tile<KIND, KS>(buf[s], dr, wave + NW * s, c, g, koff);
+    if (s < my_n) load_tile<KIND, KS, VEC>(buf[s], dr, wave + NW * s, c, g, koff);
   for (int i0 = 0; i0 < my_n; i0 += P) {
 #pragma unroll
     for (int s = 0; s < P; ++s) {
@@ -131,18 +139,15 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
             if (has_partial && t == tp) af[t] &= pmask;
           }
         }
-        float sc[4], mn[4];
+        float sc[4], off[4];
         if constexpr (U8) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            sc[r] = tile_scale(buf[s].s, r);
-            mn[r] = tile_scale(buf[s].m, r);
-          }
+          for (int r = 0; r < 4; ++r) tile_affine(buf[s].s, buf[s].m, r, sc[r], off[r]);
         }
         // The registers of slot s are free once converted: refill them now so
-        // the load overlaps this tile's MFMAs.
-        if (i + P < my_n) load_tile<KIND, KS>(buf[s], dr, wave + NW * (i + P), c, g, koff);
-
+        // the load overlaps this tile's MFMAs. (Loading past the doc instead of
+        // branching costs more: those loads still queue behind the real ones.)
+        if (i + P < my_n) load_tile<KIND, KS, VEC>(buf[s], dr, wave + NW * (i + P), c, g, koff);
         const int row0 = tile * 16 + 4 * g;
         const bool tail = tile * 16 + 16 > len;
 #pragma unroll
@@ -152,7 +157,7 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
           for (int t = 0; t < KS; ++t) acc = mfma16x16x32<BF>(af[t], qf[nb][t], acc);
           if constexpr (U8) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] = fmaf(sc[r], acc[r], mn[r] * qsum[nb]);
+            for (int r = 0; r < 4; ++r) acc[r] = fmaf(sc[r], acc[r], off[r] * qsum[nb]);
           }
           if (tail) {
 #pragma unroll
@@ -168,7 +173,7 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
               }
             }
           } else {
-            m[nb] = fmaxf(m[nb], fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3])));
+            m[nb] = vmax(m[nb], vmax(vmax(acc[0], acc[1]), vmax(acc[2], acc[3])));
           }
         }
       }
@@ -187,7 +192,7 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
         const int oi = __shfl_xor(ix, s);
         argmax_merge(v, ix, ov, oi);
       } else {
-        v = fmaxf(v, ov);
+        v = vmax(v, ov);
       }
     }
     if (g == 0) {
@@ -206,7 +211,7 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
         if constexpr (ARGMAX) {
           argmax_merge(v, ix, red_m[w][r], red_i[w][r]);
         } else {
-          v = fmaxf(v, red_m[w][r]);
+          v = vmax(v, red_m[w][r]);
         }
       }
       const int q = q0 + r;
@@ -237,12 +242,12 @@ __global__ void __launch_bounds__(256) sum_passes_kernel(FwdArgs a, int npass) {
   a.scores[qi * a.ss_n + b * a.ss_b] = s;
 }
 
-template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX>
+template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX, bool VEC = true>
 hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
   constexpr int QROWS = NQB * 16;
   const int npass = (a.Lq + QROWS - 1) / QROWS;
   const int64_t items = (int64_t)a.Nq * a.B;
-  hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX>), dim3((unsigned)items, npass),
+  hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC>), dim3((unsigned)items, npass),
                      dim3(256), 0, s, a);
   if (npass > 1) {
     hipLaunchKernelGGL(sum_passes_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, a, npass);
@@ -254,7 +259,8 @@ template <int KIND, int NQB, int KS>
 hipError_t dispatch_flags(const FwdArgs& a, bool am, hipStream_t s) {
   if constexpr (KIND == KIND_U8) {
     (void)am;
-    return launch_one<KIND, NQB, KS, true, false>(a, s);
+    return a.vec ? launch_one<KIND, NQB, KS, true, false, true>(a, s)
+                 : launch_one<KIND, NQB, KS, true, false, false>(a, s);
   } else {
     const bool kmask = a.d != 32 * KS;
     if (kmask) return am ? launch_one<KIND, NQB, KS, true, true>(a, s) : launch_one<KIND, NQB, KS, true, false>(a, s);
@@ -278,7 +284,13 @@ hipError_t dispatch_nqb(const FwdArgs& a, bool am, hipStream_t s) {
 template <int KIND>
 hipError_t dispatch_ks(const FwdArgs& a, bool am, hipStream_t s) {
   switch (stream_fwd_ks(a.d)) {
-    case 1: return dispatch_nqb<KIND, 1>(a, am, s);
+    case 1:
+      // uint8 tiles pair k-steps: d <= 32 runs as two, the second reading zeros.
+      if constexpr (KIND == KIND_U8) {
+        return dispatch_nqb<KIND, 2>(a, am, s);
+      } else {
+        return dispatch_nqb<KIND, 1>(a, am, s);
+      }
     case 2: return dispatch_nqb<KIND, 2>(a, am, s);
     case 4: return dispatch_nqb<KIND, 4>(a, am, s);
     case 8: return dispatch_nqb<KIND, 8>(a, am, s);

@@ -28,7 +28,8 @@ struct FwdArgs {
   int Nq, B, Lq, Ld, d;
   int Lq_rows;                // rows of Q (= Lq unless qidx gathers from a longer Q)
   int shared_docs;            // doc row of (query qi, doc b) is b, else qi*B + b
-  int sm_vec;                 // scales/mins may be read 4 tokens per load
+  int vec;                    // uint8 docs: 16-byte aligned code rows and scales/mins
+                              // readable 4 tokens per 8-byte load (compile-time path)
 };
 
 // Backward of the single-query forward with saved argmax.

@@ -5,6 +5,13 @@
 // for uint8 docs, the fp16 scale and min of tokens tile*16 + 4g .. +3 (the rows
 // it owns in the MFMA result layout). Tokens at or past the doc length, and
 // k >= d, come back as zeros from the buffer range check.
+//
+// Fragment slot t of lane group g covers k = frag_k0(t, g) .. +7:
+//  * fp16/bf16: 32t + 8g, one 16-byte load per slot;
+//  * uint8: slots are paired, 64*(t/2) + 16g + 8*(t%2), so one 16-byte load of
+//    16 codes feeds slots t and t+1 and a wave's load instruction covers 64
+//    contiguous bytes of each of 16 rows (KS is even for uint8 docs).
+// The query operand is loaded with the same k order, so Q * D^T is unchanged.
 #pragma once
 
 #include <type_traits>
@@ -14,10 +21,32 @@
 
 namespace fmx {
 
+template <int KIND>
+__device__ __forceinline__ int frag_k0(int t, int g) {
+  if constexpr (KIND == KIND_U8) {
+    return 64 * (t >> 1) + 16 * g + 8 * (t & 1);
+  } else {
+    return 32 * t + 8 * g;
+  }
+}
+
+// Fragment slot (t, g) whose 8 k values start at k (k a multiple of 8).
+template <int KIND>
+__device__ __forceinline__ void frag_slot(int k, int& t, int& g) {
+  if constexpr (KIND == KIND_U8) {
+    t = 2 * (k >> 6) + ((k >> 3) & 1);
+    g = (k >> 4) & 3;
+  } else {
+    t = k >> 5;
+    g = (k >> 3) & 3;
+  }
+}
+
 template <int KIND, int KS>
 struct Tile {
   static constexpr bool kU8 = KIND == KIND_U8;
-  typename std::conditional<kU8, u32x2_t, u32x4_t>::type v[KS];
+  static_assert(!kU8 || KS % 2 == 0, "uint8 tiles pair their k-steps");
+  u32x4_t v[kU8 ? KS / 2 : KS];
   u32x2_t s, m;  // uint8 docs only: fp16 bits of 4 consecutive tokens
 };
 
@@ -26,20 +55,21 @@ struct DocRes {
   rsrc_t d;       // token rows, num_records = len * row bytes
   rsrc_t s, m;    // uint8 docs: scales / mins of the doc
   uint32_t rowb;  // bytes per token row
-  int sm_vec;     // scales/mins are read 4 tokens per 8-byte load
 };
 
-template <int KIND>
+// VEC (uint8 docs; FwdArgs::vec): code rows are 16-byte aligned and
+// scales/mins are read 4 tokens per 8-byte load. Otherwise codes are read 8
+// bytes and scales 2 bytes at a time. fp16/bf16 docs always use 16-byte loads.
+template <int KIND, bool VEC>
 __device__ __forceinline__ DocRes make_doc_res(const void* D, int64_t drow, int64_t sd_b, int64_t sd_l,
                                                int len, const uint16_t* scales, const uint16_t* mins,
-                                               int64_t sm_b, int sm_vec) {
+                                               int64_t sm_b) {
   constexpr int ESZ = KindInfo<KIND>::esz;
   DocRes r;
   r.rowb = (uint32_t)(sd_l * ESZ);
   r.d = make_rsrc((const char*)D + drow * sd_b * ESZ, (uint32_t)len * r.rowb);
-  r.sm_vec = sm_vec;
   if constexpr (KIND == KIND_U8) {
-    const uint32_t n = sm_vec ? (uint32_t)((len + 3) & ~3) : (uint32_t)len;
+    const uint32_t n = VEC ? (uint32_t)((len + 3) & ~3) : (uint32_t)len;
     r.s = make_rsrc(scales + drow * sm_b, n * 2u);
     r.m = make_rsrc(mins + drow * sm_b, n * 2u);
   } else {
@@ -49,21 +79,28 @@ __device__ __forceinline__ DocRes make_doc_res(const void* D, int64_t drow, int6
   return r;
 }
 
-template <int KIND, int KS>
+template <int KIND, int KS, bool VEC>
 __device__ __forceinline__ void load_tile(Tile<KIND, KS>& T, const DocRes& r, int tile, int c, int g,
                                           const uint32_t (&koff)[KS]) {
   const uint32_t base = (uint32_t)(tile * 16 + c) * r.rowb;
+  if constexpr (KIND == KIND_U8) {
 #pragma unroll
-  for (int t = 0; t < KS; ++t) {
-    if constexpr (KIND == KIND_U8) {
-      T.v[t] = ld8(r.d, base + koff[t]);
-    } else {
-      T.v[t] = ld16(r.d, base + koff[t]);
+    for (int h = 0; h < KS / 2; ++h) {
+      if constexpr (VEC) {
+        T.v[h] = ld16(r.d, base + koff[2 * h]);
+      } else {
+        const u32x2_t lo = ld8(r.d, base + koff[2 * h]);
+        const u32x2_t hi = ld8(r.d, base + koff[2 * h + 1]);
+        T.v[h] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+      }
     }
+  } else {
+#pragma unroll
+    for (int t = 0; t < KS; ++t) T.v[t] = ld16(r.d, base + koff[t]);
   }
   if constexpr (KIND == KIND_U8) {
     const uint32_t o = (uint32_t)(tile * 16 + 4 * g) * 2u;
-    if (r.sm_vec) {
+    if constexpr (VEC) {
       T.s = ld8(r.s, o);
       T.m = ld8(r.m, o);
     } else {
@@ -86,20 +123,29 @@ __device__ __forceinline__ uint32_t query_row_offset(const FwdArgs& a, int b, in
   return (uint32_t)((int64_t)row * a.sq_l * 2);
 }
 
-// A-operand fragment of k-step t as fp16/bf16 bits.
+// Doc-operand fragment of k-step t as fp16/bf16 bits; uint8 codes come out
+// biased (1024 + code, see codes_to_f16_biased).
 template <int KIND, int KS>
 __device__ __forceinline__ u32x4_t tile_operand(const Tile<KIND, KS>& T, int t) {
   if constexpr (KIND == KIND_U8) {
-    return codes_to_f16(T.v[t]);
+    const u32x4_t w = T.v[t >> 1];
+    return codes_to_f16_biased((t & 1) ? u32x2_t{w[2], w[3]} : u32x2_t{w[0], w[1]});
   } else {
     return T.v[t];
   }
 }
 
-// fp32 scale and min of result row i (0..3) of this lane (uint8 docs).
+// fp32 scale of result row i (0..3) of this lane (uint8 docs).
 __device__ __forceinline__ float tile_scale(u32x2_t s, int i) {
   const uint32_t w = s[i >> 1];
   return half_bits_to_float((i & 1) ? (w >> 16) : (w & 0xffffu));
+}
+
+// Affine epilogue constants of result row i: with biased codes,
+// S = scale * U + (min - 1024 * scale) * sum(Q); returns (scale, min - 1024 * scale).
+__device__ __forceinline__ void tile_affine(const u32x2_t& s, const u32x2_t& m, int i, float& sc, float& off) {
+  sc = tile_scale(s, i);
+  off = fmaf(-kCodeBias, sc, tile_scale(m, i));
 }
 
 }  // namespace fmx
