@@ -23,6 +23,9 @@ ARCH = os.environ.get("FMX_OFFLOAD_ARCH", "gfx950")
 
 # Packed fp32 VALU ops are disabled: hand-rolled or compiler-formed
 # v_pk_{add,mul,fma}_f32 are not used anywhere in this library.
+# MFMAs accumulate in VGPRs (gfx950's unified register file) rather than AGPRs:
+# the epilogues read every result, and the AGPR form costs a v_accvgpr_read
+# per result register.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -34,6 +37,8 @@ HIP_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
 ]
 
 

@@ -119,19 +119,17 @@ __device__ __forceinline__ float bf16_bits_to_float(uint32_t bits16) {
   return __builtin_bit_cast(float, bits16 << 16);
 }
 
-// Sum of the 8 fp16 / bf16 elements packed in a fragment, in fp32.
-template <bool BF>
-__device__ __forceinline__ float frag_sum(u32x4_t v) {
-  float s = 0.f;
+// Row sums of a 16-token fp16 query block held as B-fragments qf[0..KS-1]:
+// an MFMA against an all-ones A operand puts sum_k Q[c, k] (fp32 accumulate)
+// in every result row of column c, so lane (c, g) gets its query token's sum
+// in KS matrix instructions instead of 16 VALU ops per fragment.
+template <int KS>
+__device__ __forceinline__ float query_row_sum(const u32x4_t (&qf)[KS]) {
+  const u32x4_t ones = {0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};  // fp16 1.0
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    if constexpr (BF) {
-      s += bf16_bits_to_float(v[w] & 0xffffu) + bf16_bits_to_float(v[w] >> 16);
-    } else {
-      s += half_bits_to_float(v[w] & 0xffffu) + half_bits_to_float(v[w] >> 16);
-    }
-  }
-  return s;
+  for (int t = 0; t < KS; ++t) acc = mfma16x16x32<false>(ones, qf[t], acc);
+  return acc[0];
 }
 
 // Mask keeping the first n (0..8) 16-bit elements of an 8-element fragment.

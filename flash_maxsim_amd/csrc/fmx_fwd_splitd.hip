@@ -85,11 +85,7 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
   if constexpr (U8) {
 #pragma unroll
     for (int nb = 0; nb < NQB; ++nb) {
-      float s = 0.f;
-#pragma unroll
-      for (int t = 0; t < KSW; ++t) s += frag_sum<false>(qf[nb][t]);
-      s += __shfl_xor(s, 16);
-      s += __shfl_xor(s, 32);
+      const float s = query_row_sum<KSW>(qf[nb]);
       if (g == 0) qs_part[wave][nb * 16 + c] = s;
     }
     __syncthreads();

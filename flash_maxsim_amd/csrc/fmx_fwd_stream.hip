@@ -94,12 +94,7 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
     }
     qsum[nb] = 0.f;
     if constexpr (U8) {
-      float s = 0.f;
-#pragma unroll
-      for (int t = 0; t < KS; ++t) s += frag_sum<false>(qf[nb][t]);
-      s += __shfl_xor(s, 16);
-      s += __shfl_xor(s, 32);
-      qsum[nb] = s;
+      qsum[nb] = query_row_sum<KS>(qf[nb]);
     }
   }
 

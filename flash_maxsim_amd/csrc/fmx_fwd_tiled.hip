@@ -338,11 +338,20 @@ hipError_t dispatch_flags(const FwdArgs& a, const TiledPlan& p, bool am, hipStre
 template <int KIND>
 hipError_t dispatch(const FwdArgs& a, const TiledPlan& p, bool am, hipStream_t s) {
   if (p.ks == 4) {
-    if (p.nb == 8) return dispatch_flags<KIND, kTiledNW, 8, 4>(a, p, am, s);
-    if (p.nb == 4) return dispatch_flags<KIND, kTiledNW, 4, 4>(a, p, am, s);
+    switch (p.nb) {
+      case 8: return dispatch_flags<KIND, kTiledNW, 8, 4>(a, p, am, s);
+      case 6: return dispatch_flags<KIND, kTiledNW, 6, 4>(a, p, am, s);
+      case 5: return dispatch_flags<KIND, kTiledNW, 5, 4>(a, p, am, s);
+      case 4: return dispatch_flags<KIND, kTiledNW, 4, 4>(a, p, am, s);
+      default: break;
+    }
   } else if (p.ks == 8) {
-    if (p.nb == 4) return dispatch_flags<KIND, kTiledNW, 4, 8>(a, p, am, s);
-    if (p.nb == 2) return dispatch_flags<KIND, kTiledNW, 2, 8>(a, p, am, s);
+    switch (p.nb) {
+      case 4: return dispatch_flags<KIND, kTiledNW, 4, 8>(a, p, am, s);
+      case 3: return dispatch_flags<KIND, kTiledNW, 3, 8>(a, p, am, s);
+      case 2: return dispatch_flags<KIND, kTiledNW, 2, 8>(a, p, am, s);
+      default: break;
+    }
   }
   return hipErrorInvalidValue;
 }
@@ -353,22 +362,25 @@ bool tiled_fwd_applicable(int64_t Nq, int64_t Lq, int d) { return d >= 1 && d <=
 
 // Picks rows per wave (NB) and doc groups (G). `slots` workgroups run at once
 // (kTiledWPC per CU, two waves per SIMD). The slowest workgroup's MFMA time is
-// proportional to docs-per-group x rows-per-block. The XCD-aware mapping puts
-// all row blocks of a doc group on one XCD (G a multiple of 8, nRB * G / 8
-// workgroups per XCD), so each doc tile is fetched once per XCD L2; without
-// it the row blocks of a doc meet in the shared last-level cache instead,
-// which is counted as a few percent of extra cost.
+// proportional to docs-per-group x rows-per-block, so NB is chosen to cut the
+// flattened query rows into nearly full row blocks (3200 rows of config 3:
+// five blocks of 640, where 512-row blocks leave a quarter-full seventh and
+// idle CUs). The XCD-aware mapping puts all row blocks of a doc group on one
+// XCD (G a multiple of 8, nRB * G / 8 workgroups per XCD), so each doc tile is
+// fetched once per XCD L2; without it the row blocks of a doc meet in the
+// shared last-level cache instead, which is counted as a few percent of extra
+// cost.
 TiledPlan tiled_fwd_plan(int64_t Nq, int64_t B, int64_t Lq, int d, int cus) {
   TiledPlan best = {};
   const int ks = d <= 128 ? 4 : 8;
-  const int nbs4[2] = {8, 4}, nbs8[2] = {4, 2};
+  const int nbs4[4] = {8, 6, 5, 4}, nbs8[4] = {4, 3, 2, 2};
   const int* nbs = ks == 4 ? nbs4 : nbs8;
   const int slots = (cus > 0 ? cus : 256) * kTiledWPC;
   const int per_xcd = slots / 8;
   const int64_t rows = Nq * Lq;
   double best_cost = 0;
   bool have = false;
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < 4; ++i) {
     for (int xcd = 1; xcd >= 0; --xcd) {
       TiledPlan p = {};
       p.ks = ks;

@@ -384,6 +384,23 @@ def test_tiled_shapes(oracle_mod, Nq, Lq, B, Ld, d):
     assert_scores(out, ref)
 
 
+@pytest.mark.parametrize("Nq, Lq, B, Ld, d", [
+    (100, 32, 300, 40, 128),    # 3200 rows: five 640-row blocks (NB = 5)
+    (24, 32, 300, 50, 128),     # 768 rows: one 768-row block (NB = 6)
+    (12, 32, 300, 64, 256),     # d = 256, 384 rows (NB = 3)
+])
+def test_tiled_row_block_sizes(oracle_mod, Nq, Lq, B, Ld, d):
+    # Shapes whose plan (256 CUs) picks each row-block size; the oracle checks
+    # every fourth query (first and last included) to stay within seconds.
+    Q = sim((Nq, Lq, d), 900 + Nq)
+    D = sim((B, Ld, d), 901 + d)
+    lengths = torch.randint(0, Ld + 5, (B,), generator=torch.Generator().manual_seed(Nq), dtype=torch.int32)
+    out = fm.flash_maxsim_batched(Q.to(DEV), D.to(DEV), lengths.to(DEV))
+    pick = sorted(set(range(0, Nq, 4)) | {Nq - 1})
+    ref = oracle_mod.maxsim(to_np32(Q[pick]), to_np32(D), lengths.numpy())
+    assert_scores(out[pick], ref)
+
+
 def test_tiled_bf16_and_argmax(oracle_mod):
     s, dQ, dD, ref, am_ref, best, Qn, Dn, g = run_train(oracle_mod, 6, 512, 100, 128, 820, torch.bfloat16)
     assert_scores(s, ref[0])
