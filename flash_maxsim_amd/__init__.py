@@ -4,6 +4,9 @@ Drop-in for the reference package flash_maxsim 0.1.0
 (flash_maxsim/__init__.py:1-5): the same nine callables with the same
 signatures. ``import flash_maxsim_amd as flash_maxsim`` keeps existing call
 sites unchanged.
+
+Beyond the reference: packed variable-length docs (pack_docs,
+quantize_int8_packed, flash_maxsim_packed, flash_maxsim_int8_packed).
 """
 
 __version__ = "0.1.0"
@@ -11,6 +14,8 @@ __version__ = "0.1.0"
 from .flash_maxsim import flash_maxsim, flash_maxsim_batched, flash_maxsim_train, maxsim_naive
 from .flash_maxsim_quant import flash_maxsim_int8, quantize_int8, dequantize_int8
 from .flash_maxsim_sparse import flash_maxsim_sparse, maxsim_sparse_naive
+from .flash_maxsim_packed import (PackedDocs, PackedInt8Docs, flash_maxsim_int8_packed, flash_maxsim_packed,
+                                  pack_docs, quantize_int8_packed)
 
 __all__ = [
     "flash_maxsim",
@@ -22,4 +27,10 @@ __all__ = [
     "dequantize_int8",
     "flash_maxsim_sparse",
     "maxsim_sparse_naive",
+    "PackedDocs",
+    "PackedInt8Docs",
+    "pack_docs",
+    "quantize_int8_packed",
+    "flash_maxsim_packed",
+    "flash_maxsim_int8_packed",
 ]

@@ -16,6 +16,7 @@ LIB_PATH = Path(__file__).resolve().with_name("libflashmaxsim.so")
 
 FMX_DTYPE_F16 = 0
 FMX_DTYPE_BF16 = 1
+FMX_DTYPE_F32 = 2
 
 _i64 = ctypes.c_int64
 _ptr = ctypes.c_void_p
@@ -44,6 +45,20 @@ _SIGNATURES = {
          _i64, _i64, _i64, _ptr, _size, _ptr],
     ),
     "fmx_fwd_sparse_workspace_bytes": (_size, [_i64, _i64, _i64, _i64]),
+    "fmx_quantize_int8": (
+        _int,
+        [_int, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr, _i64, _ptr, _ptr, _i64, _ptr],
+    ),
+    "fmx_fwd_packed": (
+        _int,
+        [_int, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _ptr, _i64, _i64, _i64, _ptr, _size, _ptr],
+    ),
+    "fmx_fwd_packed_workspace_bytes": (_size, [_i64, _i64, _i64, _i64]),
+    "fmx_fwd_int8_packed": (
+        _int,
+        [_ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr, _i64, _ptr, _ptr, _ptr, _i64, _i64, _i64, _ptr, _size, _ptr],
+    ),
+    "fmx_fwd_int8_packed_workspace_bytes": (_size, [_i64, _i64, _i64, _i64]),
     "fmx_bwd": (
         _int,
         [_int, _ptr, _i64, _ptr, _i64, _i64, _ptr, _ptr, _ptr, _ptr,

@@ -127,11 +127,15 @@ size_t fmx_fwd_int8_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld, int64_t d
   return stream_ws_bytes(1, B, Lq, d);
 }
 
-int fmx_fwd(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, const void* D,
-            int64_t d_stride_b, int64_t d_stride_l, const int32_t* lengths, float* scores,
-            int64_t s_stride_n, int64_t s_stride_b, int32_t* argmax, int64_t Nq, int64_t B,
-            int64_t Lq, int64_t Ld, int64_t d, int shared_docs, void* workspace,
-            size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// fmx_fwd and fmx_fwd_packed: tok_group non-null selects packed docs.
+int fwd_impl(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, const void* D, int64_t d_stride_b,
+             int64_t d_stride_l, const int64_t* tok_group, int64_t tok_rows, const int32_t* lengths, float* scores,
+             int64_t s_stride_n, int64_t s_stride_b, int32_t* argmax, int64_t Nq, int64_t B, int64_t Lq, int64_t Ld,
+             int64_t d, int shared_docs, void* workspace, size_t workspace_bytes, void* stream) {
   if (dtype != FMX_DTYPE_F16 && dtype != FMX_DTYPE_BF16) return fail(FMX_ERR_INVALID, "unknown dtype %d", dtype);
   int rc = check_common(Nq, B, Lq, Ld, d, q_stride_l, d_stride_b, d_stride_l, 2);
   if (rc) return rc;
@@ -158,6 +162,8 @@ int fmx_fwd(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, co
   a.scores = scores;
   a.argmax = argmax;
   a.partial = static_cast<float*>(workspace);
+  a.tok_group = tok_group;
+  a.tok_rows = tok_rows;
   a.sq_n = Nq > 1 ? q_stride_n : 0;
   a.sq_l = q_stride_l;
   a.sd_b = d_stride_b;
@@ -184,10 +190,11 @@ int fmx_fwd(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, co
   return hip_status(e, "fmx_fwd launch");
 }
 
-int fmx_fwd_int8(const void* Q, int64_t q_stride_l, const uint8_t* D, int64_t d_stride_b,
-                 int64_t d_stride_l, const void* scales, const void* mins, int64_t sm_stride_b,
-                 const int32_t* lengths, float* scores, int64_t B, int64_t Lq, int64_t Ld, int64_t d,
-                 void* workspace, size_t workspace_bytes, void* stream) {
+// fmx_fwd_int8 and fmx_fwd_int8_packed: tok_group non-null selects packed docs.
+int int8_impl(const void* Q, int64_t q_stride_l, const uint8_t* D, int64_t d_stride_b, int64_t d_stride_l,
+              const void* scales, const void* mins, int64_t sm_stride_b, const int64_t* tok_group, int64_t tok_rows,
+              const int32_t* lengths, float* scores, int64_t B, int64_t Lq, int64_t Ld, int64_t d, void* workspace,
+              size_t workspace_bytes, void* stream) {
   int rc = check_common(1, B, Lq, Ld, d, q_stride_l, d_stride_b, d_stride_l, 1);
   if (rc) return rc;
   if (B == 0) return ok();
@@ -196,7 +203,8 @@ int fmx_fwd_int8(const void* Q, int64_t q_stride_l, const uint8_t* D, int64_t d_
   if (!aligned16(Q) || !aligned16(D)) return fail(FMX_ERR_INVALID, "Q and D must be 16-byte aligned");
   if ((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(mins)) & 1u)
     return fail(FMX_ERR_INVALID, "scales and mins must be 2-byte aligned");
-  if (sm_stride_b < Ld) return fail(FMX_ERR_INVALID, "scale doc stride %lld < Ld", (long long)sm_stride_b);
+  if (!tok_group && sm_stride_b < Ld)
+    return fail(FMX_ERR_INVALID, "scale doc stride %lld < Ld", (long long)sm_stride_b);
   const size_t need = stream_ws_bytes(1, B, Lq, d);
   if (need > 0 && (!workspace || workspace_bytes < need))
     return fail(FMX_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
@@ -210,6 +218,8 @@ int fmx_fwd_int8(const void* Q, int64_t q_stride_l, const uint8_t* D, int64_t d_
   a.scales = static_cast<const uint16_t*>(scales);
   a.mins = static_cast<const uint16_t*>(mins);
   a.partial = static_cast<float*>(workspace);
+  a.tok_group = tok_group;
+  a.tok_rows = tok_rows;
   a.sq_n = 0;
   a.sq_l = q_stride_l;
   a.sd_b = d_stride_b;
@@ -225,16 +235,117 @@ int fmx_fwd_int8(const void* Q, int64_t q_stride_l, const uint8_t* D, int64_t d_
   a.d = (int)d;
   a.shared_docs = 1;
   // The vector path reads codes 16 bytes at a time (16-byte aligned rows) and
-  // four scales per 8-byte load, which needs 8-byte aligned doc rows of scales
-  // and a padded length that never passes the end of a doc's row.
-  a.vec = ((d_stride_b & 15) == 0 && (d_stride_l & 15) == 0 && (sm_stride_b & 3) == 0 && (Ld & 3) == 0 &&
-           ((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(mins)) & 7u) == 0)
-              ? 1
-              : 0;
+  // four scales per 8-byte load, which needs 8-byte aligned scale rows and a
+  // padded length that never passes the end of a doc's scales: Ld % 4 == 0 for
+  // padded docs; packed docs start on 4-token groups, whose rows are the doc's.
+  const bool sm8 = ((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(mins)) & 7u) == 0;
+  const bool rows16 = (d_stride_l & 15) == 0 && (tok_group || (d_stride_b & 15) == 0);
+  a.vec = (rows16 && sm8 && (tok_group || ((sm_stride_b & 3) == 0 && (Ld & 3) == 0))) ? 1 : 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const hipError_t e = plan_fwd(Lq, d).splitd ? fmx::launch_splitd_fwd(fmx::KIND_U8, a, false, s)
                                               : fmx::launch_stream_fwd(fmx::KIND_U8, a, false, s);
   return hip_status(e, "fmx_fwd_int8 launch");
+}
+
+int check_packed(const int64_t* tok_group, const int32_t* lengths, int64_t tok_rows) {
+  if (!tok_group || !lengths) return fail(FMX_ERR_INVALID, "packed docs need tok_group and lengths");
+  if (tok_rows < 0) return fail(FMX_ERR_INVALID, "tok_rows=%lld must be >= 0", (long long)tok_rows);
+  return FMX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fmx_fwd(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, const void* D,
+            int64_t d_stride_b, int64_t d_stride_l, const int32_t* lengths, float* scores,
+            int64_t s_stride_n, int64_t s_stride_b, int32_t* argmax, int64_t Nq, int64_t B,
+            int64_t Lq, int64_t Ld, int64_t d, int shared_docs, void* workspace,
+            size_t workspace_bytes, void* stream) {
+  return fwd_impl(dtype, Q, q_stride_n, q_stride_l, D, d_stride_b, d_stride_l, nullptr, 0, lengths, scores,
+                  s_stride_n, s_stride_b, argmax, Nq, B, Lq, Ld, d, shared_docs, workspace, workspace_bytes, stream);
+}
+
+int fmx_fwd_int8(const void* Q, int64_t q_stride_l, const uint8_t* D, int64_t d_stride_b,
+                 int64_t d_stride_l, const void* scales, const void* mins, int64_t sm_stride_b,
+                 const int32_t* lengths, float* scores, int64_t B, int64_t Lq, int64_t Ld, int64_t d,
+                 void* workspace, size_t workspace_bytes, void* stream) {
+  return int8_impl(Q, q_stride_l, D, d_stride_b, d_stride_l, scales, mins, sm_stride_b, nullptr, 0, lengths, scores,
+                   B, Lq, Ld, d, workspace, workspace_bytes, stream);
+}
+
+size_t fmx_fwd_packed_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld_max, int64_t d) {
+  return fwd_ws_bytes(1, B, Lq, d);
+}
+
+int fmx_fwd_packed(int dtype, const void* Q, int64_t q_stride_l, int64_t Lq, const void* D, int64_t d_stride_l,
+                   int64_t tok_rows, const int64_t* tok_group, const int32_t* lengths, float* scores, int64_t B,
+                   int64_t Ld_max, int64_t d, void* workspace, size_t workspace_bytes, void* stream) {
+  if (B > 0) {
+    const int rc = check_packed(tok_group, lengths, tok_rows);
+    if (rc) return rc;
+  }
+  return fwd_impl(dtype, Q, 0, q_stride_l, D, 0, d_stride_l, tok_group, tok_rows, lengths, scores, 0, 1, nullptr,
+                  1, B, Lq, Ld_max, d, 1, workspace, workspace_bytes, stream);
+}
+
+size_t fmx_fwd_int8_packed_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld_max, int64_t d) {
+  return stream_ws_bytes(1, B, Lq, d);
+}
+
+int fmx_fwd_int8_packed(const void* Q, int64_t q_stride_l, int64_t Lq, const uint8_t* codes, int64_t c_stride_l,
+                        const void* scales, const void* mins, int64_t tok_rows, const int64_t* tok_group,
+                        const int32_t* lengths, float* scores, int64_t B, int64_t Ld_max, int64_t d,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  if (B > 0) {
+    const int rc = check_packed(tok_group, lengths, tok_rows);
+    if (rc) return rc;
+  }
+  return int8_impl(Q, q_stride_l, codes, 0, c_stride_l, scales, mins, 0, tok_group, tok_rows, lengths, scores, B,
+                   Lq, Ld_max, d, workspace, workspace_bytes, stream);
+}
+
+int fmx_quantize_int8(int src_dtype, const void* src, int64_t s_stride_b, int64_t s_stride_l, int64_t B, int64_t Ld,
+                      int64_t d, const int32_t* lengths, const int64_t* tok_group, uint8_t* codes,
+                      int64_t c_stride_l, void* scales, void* mins, int64_t sm_stride_b, void* stream) {
+  int esz;
+  switch (src_dtype) {
+    case FMX_DTYPE_F16: esz = 2; break;
+    case FMX_DTYPE_BF16: esz = 2; break;
+    case FMX_DTYPE_F32: esz = 4; break;
+    default: return fail(FMX_ERR_INVALID, "unknown source dtype %d", src_dtype);
+  }
+  if (B < 0 || Ld < 0 || d < 1 || d > FMX_MAX_D)
+    return fail(FMX_ERR_INVALID, "invalid sizes B=%lld Ld=%lld d=%lld", (long long)B, (long long)Ld, (long long)d);
+  if (s_stride_l < d || c_stride_l < d || s_stride_b < 0)
+    return fail(FMX_ERR_INVALID, "row strides must be >= d");
+  if (!tok_group && (sm_stride_b < Ld)) return fail(FMX_ERR_INVALID, "scale doc stride < Ld");
+  if (B == 0 || Ld == 0) return ok();
+  if (!src || !codes || !scales || !mins) return fail(FMX_ERR_INVALID, "src, codes, scales and mins must be non-null");
+  if ((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(mins)) & 1u)
+    return fail(FMX_ERR_INVALID, "scales and mins must be 2-byte aligned");
+  if (reinterpret_cast<uintptr_t>(src) % esz) return fail(FMX_ERR_INVALID, "src must be aligned to its element");
+  fmx::QuantArgs a = {};
+  a.src = src;
+  a.s_stride_b = s_stride_b;
+  a.s_stride_l = s_stride_l;
+  a.B = B;
+  a.Ld = Ld;
+  a.d = d;
+  a.esz = esz;
+  a.lengths = lengths;
+  a.tok_group = tok_group;
+  a.codes = codes;
+  a.c_stride_l = c_stride_l;
+  a.scales = scales;
+  a.mins = mins;
+  a.sm_stride_b = sm_stride_b;
+  a.vec = (aligned16(src) && ((s_stride_b * esz) & 15) == 0 && ((s_stride_l * esz) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(codes) & 7u) == 0 && (c_stride_l & 7) == 0)
+              ? 1
+              : 0;
+  const int kind = src_dtype == FMX_DTYPE_F32 ? 2 : (src_dtype == FMX_DTYPE_BF16 ? 1 : 0);
+  return hip_status(fmx::launch_quantize(kind, a, static_cast<hipStream_t>(stream)), "fmx_quantize_int8 launch");
 }
 
 size_t fmx_fwd_sparse_workspace_bytes(int64_t B, int64_t K, int64_t Ld, int64_t d) {

@@ -96,7 +96,7 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
   }
 
   // ---- doc stream ----
-  const DocRes dr = make_doc_res<KIND, VEC>(a.D, drow, a.sd_b, a.sd_l, len, a.scales, a.mins, a.sm_b);
+  const DocRes dr = make_doc_res<KIND, VEC>(a, drow, len);
   uint32_t koff[KSW];
 #pragma unroll
   for (int t = 0; t < KSW; ++t) {

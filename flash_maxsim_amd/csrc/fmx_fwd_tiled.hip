@@ -144,7 +144,17 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
   // ---- tile loader: chunk k of this thread = tid + k*512 -> (row, 16-byte column) ----
   const uint32_t rowb = (uint32_t)(a.sd_l * 2);
   auto tile_rsrc = [&](int b, int len) {
-    return make_rsrc(static_cast<const char*>(a.D) + (int64_t)b * a.sd_b * 2, (uint32_t)len * rowb);
+    int64_t rows = len;
+    const char* base = static_cast<const char*>(a.D);
+    if (a.tok_group) {  // packed docs: clamp to the rows of D
+      const int64_t t0 = 4 * a.tok_group[b];
+      const int64_t avail = t0 < 0 ? 0 : (a.tok_rows > t0 ? a.tok_rows - t0 : 0);
+      if (rows > avail) rows = avail;
+      if (avail > 0) base += doc_elem0(a, b) * 2;
+    } else {
+      base += doc_elem0(a, b) * 2;
+    }
+    return make_rsrc(base, (uint32_t)rows * rowb);
   };
   auto doc_len = [&](int b) {
     int l = a.lengths ? a.lengths[b] : a.Ld;

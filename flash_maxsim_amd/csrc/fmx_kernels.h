@@ -27,6 +27,9 @@ struct FwdArgs {
   int64_t sm_b;
   int Nq, B, Lq, Ld, d;
   int Lq_rows;                // rows of Q (= Lq unless qidx gathers from a longer Q)
+  const int64_t* tok_group;   // packed docs: doc row r starts at token row 4*tok_group[r]
+                              // (then sd_b and sm_b are unused), or null
+  int64_t tok_rows;           // packed docs: token rows in D (reads are clamped to them)
   int shared_docs;            // doc row of (query qi, doc b) is b, else qi*B + b
   int vec;                    // uint8 docs: 16-byte aligned code rows and scales/mins
                               // readable 4 tokens per 8-byte load (compile-time path)
@@ -79,6 +82,23 @@ bool tiled_fwd_applicable(int64_t Nq, int64_t Lq, int d);
 TiledPlan tiled_fwd_plan(int64_t Nq, int64_t B, int64_t Lq, int d, int cus);
 size_t tiled_fwd_workspace_bytes(const TiledPlan& p, int64_t Nq, int64_t B);
 hipError_t launch_tiled_fwd(int kind, const FwdArgs& a, const TiledPlan& p, bool with_argmax, hipStream_t s);
+
+// Per-token uint8 quantisation (the encoder of the uint8 doc format).
+struct QuantArgs {
+  const void* src;            // [B, Ld, d] fp16 / bf16 / fp32, strides s_stride_b, s_stride_l
+  int64_t s_stride_b, s_stride_l;
+  int64_t B, Ld, d;
+  int esz;                    // bytes per source element
+  const int32_t* lengths;     // [B] valid tokens per doc (packed output), or null (= Ld)
+  const int64_t* tok_group;   // packed output: doc b starts at row 4*tok_group[b]; null = padded
+  uint8_t* codes;             // padded [B, Ld, d] (row b*Ld + j) or packed [T, d]; row stride c_stride_l
+  int64_t c_stride_l;
+  void* scales;               // fp16 bits: padded [B, Ld] (doc stride sm_stride_b) or packed [T]
+  void* mins;
+  int64_t sm_stride_b;
+  int vec;                    // 16-byte source rows and 8-byte code rows: vector loads/stores
+};
+hipError_t launch_quantize(int src_kind, const QuantArgs& a, hipStream_t s);  // 0 f16, 1 bf16, 2 f32
 
 // dQ / dD of the argmax backward.
 int bwd_dq_chunks(int B, int Lq, int d);

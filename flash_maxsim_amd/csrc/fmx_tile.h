@@ -57,21 +57,35 @@ struct DocRes {
   uint32_t rowb;  // bytes per token row
 };
 
+// First element of doc row `drow` of the document operand: drow * sd_b, or
+// for packed docs the start of its token group, 4 * tok_group[drow] rows in.
+__device__ __forceinline__ int64_t doc_elem0(const FwdArgs& a, int64_t drow) {
+  return a.tok_group ? 4 * a.tok_group[drow] * a.sd_l : drow * a.sd_b;
+}
+
 // VEC (uint8 docs; FwdArgs::vec): code rows are 16-byte aligned and
 // scales/mins are read 4 tokens per 8-byte load. Otherwise codes are read 8
 // bytes and scales 2 bytes at a time. fp16/bf16 docs always use 16-byte loads.
+// Packed docs: the rows a doc's reads may reach are clamped to the rows of D,
+// so a start past the end reads zeros instead of memory past the tensor.
 template <int KIND, bool VEC>
-__device__ __forceinline__ DocRes make_doc_res(const void* D, int64_t drow, int64_t sd_b, int64_t sd_l,
-                                               int len, const uint16_t* scales, const uint16_t* mins,
-                                               int64_t sm_b) {
+__device__ __forceinline__ DocRes make_doc_res(const FwdArgs& a, int64_t drow, int len) {
   constexpr int ESZ = KindInfo<KIND>::esz;
   DocRes r;
-  r.rowb = (uint32_t)(sd_l * ESZ);
-  r.d = make_rsrc((const char*)D + drow * sd_b * ESZ, (uint32_t)len * r.rowb);
+  r.rowb = (uint32_t)(a.sd_l * ESZ);
+  int64_t avail = INT64_MAX;  // token rows from the doc's start to the end of D
+  if (a.tok_group) {
+    const int64_t t0 = 4 * a.tok_group[drow];
+    avail = t0 < 0 ? 0 : (a.tok_rows > t0 ? a.tok_rows - t0 : 0);
+  }
+  const int64_t drows = len < avail ? len : avail;
+  r.d = make_rsrc((const char*)a.D + (avail > 0 ? doc_elem0(a, drow) * ESZ : 0), (uint32_t)drows * r.rowb);
   if constexpr (KIND == KIND_U8) {
-    const uint32_t n = VEC ? (uint32_t)((len + 3) & ~3) : (uint32_t)len;
-    r.s = make_rsrc(scales + drow * sm_b, n * 2u);
-    r.m = make_rsrc(mins + drow * sm_b, n * 2u);
+    const int64_t sm0 = a.tok_group ? (avail > 0 ? 4 * a.tok_group[drow] : 0) : drow * a.sm_b;
+    int64_t n = VEC ? (int64_t)((len + 3) & ~3) : (int64_t)len;
+    if (n > avail) n = avail;
+    r.s = make_rsrc(a.scales + sm0, (uint32_t)n * 2u);
+    r.m = make_rsrc(a.mins + sm0, (uint32_t)n * 2u);
   } else {
     r.s = r.d;
     r.m = r.d;

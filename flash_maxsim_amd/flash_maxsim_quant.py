@@ -29,11 +29,50 @@ def quantize_int8(D: torch.Tensor):
     flash_maxsim_quant.py:11-28, whose arithmetic this matches bit for bit).
     """
     assert D.dim() == 3
+    if D.is_cuda:
+        return _quantize_gpu(D)
     x = D.to(torch.float32)
     lo, hi = torch.aminmax(x, dim=-1, keepdim=True)
     step = torch.clamp_min((hi - lo) / 255.0, 1e-8)
     codes = torch.clamp(torch.round((x - lo) / step), 0, 255).to(torch.uint8)
     return codes, step.to(torch.float16), lo.to(torch.float16)
+
+
+_SRC_CODES = {torch.float16: _lib.FMX_DTYPE_F16, torch.bfloat16: _lib.FMX_DTYPE_BF16,
+              torch.float32: _lib.FMX_DTYPE_F32}
+
+
+def _quant_source(D: torch.Tensor) -> torch.Tensor:
+    """D as fp16/bf16/fp32 with unit inner stride (other dtypes go through fp32,
+    as the torch formula's D.to(float32) does)."""
+    if D.dtype not in _SRC_CODES:
+        D = D.to(torch.float32)
+    if D.stride(-1) != 1 or (D.dim() == 3 and D.shape[1] > 1 and D.stride(1) < D.shape[2]):
+        D = D.contiguous()
+    return D
+
+
+def _quantize_gpu(D: torch.Tensor):
+    """quantize_int8 in one pass of libflashmaxsim's HIP encoder; bit-identical
+    to the torch formula (same IEEE fp32 operations, same order)."""
+    B, Ld, d = D.shape
+    src = _quant_source(D)
+    dev = _check_devices(src)
+    codes = torch.empty(B, Ld, d, device=dev, dtype=torch.uint8)
+    scales = torch.empty(B, Ld, 1, device=dev, dtype=torch.float16)
+    mins = torch.empty(B, Ld, 1, device=dev, dtype=torch.float16)
+    if B == 0 or Ld == 0 or d == 0:
+        if d == 0:  # empty rows: min/max of nothing, as torch.aminmax raises
+            raise RuntimeError("quantize_int8 needs d >= 1")
+        return codes, scales, mins
+    lib = _lib.load()
+    with _device_guard(dev):
+        rc = lib.fmx_quantize_int8(
+            _SRC_CODES[src.dtype], src.data_ptr(), src.stride(0), src.stride(1), B, Ld, d, None, None,
+            codes.data_ptr(), d, scales.data_ptr(), mins.data_ptr(), Ld, _lib.stream_of(src),
+        )
+    _lib.check(rc)
+    return codes, scales, mins
 
 
 def dequantize_int8(D_uint8: torch.Tensor, scales: torch.Tensor, mins: torch.Tensor) -> torch.Tensor:

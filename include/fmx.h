@@ -39,6 +39,7 @@ extern "C" {
 
 #define FMX_DTYPE_F16 0
 #define FMX_DTYPE_BF16 1
+#define FMX_DTYPE_F32 2 /* fmx_quantize_int8 sources only */
 
 #define FMX_MAX_D 2048
 
@@ -114,6 +115,60 @@ int fmx_fwd_sparse(int dtype, const void* Q, int64_t q_stride_l, int64_t Lq, con
                    int64_t Ld, int64_t d, void* workspace, size_t workspace_bytes, void* stream);
 
 size_t fmx_fwd_sparse_workspace_bytes(int64_t B, int64_t K, int64_t Ld, int64_t d);
+
+/*
+ * Per-token uint8 quantisation (the encoder of fmx_fwd_int8's doc format):
+ * for every token row x (d values, widened to fp32)
+ *   lo = min x, step = max((max x - lo) / 255, 1e-8),
+ *   code = clamp(round_half_even((x - lo) / step), 0, 255),
+ *   scale = fp16(step), min = fp16(lo)   (round to nearest even)
+ * with IEEE fp32 operations in that order: bit-identical to the reference's
+ * torch formula.
+ *
+ *   src      [B, Ld, d]  src_dtype (F16, BF16 or F32), strides (s_stride_b, s_stride_l, 1)
+ * Padded output (tok_group NULL), the reference layout; lengths is ignored:
+ *   codes    [B, Ld, d]  uint8, token (b, j) at row b*Ld + j, row stride c_stride_l
+ *   scales   [B, Ld]     fp16, strides (sm_stride_b, 1); mins likewise
+ * Packed output (tok_group non-NULL): doc b's first len_b = lengths[b] tokens
+ * (clamped to [0, Ld]; NULL lengths = Ld) go to rows 4*tok_group[b] + j of
+ *   codes    [T, d]      uint8, row stride c_stride_l
+ *   scales   [T]         fp16; mins likewise (sm_stride_b unused)
+ * and rows len_b .. 4*ceil(len_b/4)-1 of the doc's group are zeroed. The caller
+ * lays groups out without overlap (e.g. tok_group = exclusive prefix sum of
+ * ceil(len_b / 4)); T >= 4 * (tok_group[B-1] + ceil(len_{B-1} / 4)).
+ *
+ * Replaces flash_maxsim/flash_maxsim_quant.py:11-28 (quantize_int8, torch ops
+ * there); the packed layout is an extension (no counterpart in the reference).
+ */
+int fmx_quantize_int8(int src_dtype, const void* src, int64_t s_stride_b, int64_t s_stride_l, int64_t B, int64_t Ld,
+                      int64_t d, const int32_t* lengths, const int64_t* tok_group, uint8_t* codes,
+                      int64_t c_stride_l, void* scales, void* mins, int64_t sm_stride_b, void* stream);
+
+/*
+ * Packed-doc forwards (no counterpart in the reference, whose docs are always
+ * padded [B, Ld, d]): the T token rows of all docs are stored back to back,
+ * doc b in rows 4*tok_group[b] .. 4*tok_group[b] + lengths[b] - 1, so padding
+ * costs neither storage nor reads. tok_group and lengths (int32, clamped to
+ * [0, Ld_max]) are required; reads are clamped to the T = tok_rows rows of D.
+ * Scores equal fmx_fwd / fmx_fwd_int8 (Nq = 1) on the padded equivalent.
+ *
+ *   Q        [Lq, d]   dtype (fp16 for int8), row stride q_stride_l
+ *   D/codes  [T, d]    dtype / uint8, row stride d_stride_l / c_stride_l
+ *   scales   [T]       fp16 (int8 only); mins likewise
+ *   scores   [B]       fp32, contiguous
+ */
+int fmx_fwd_packed(int dtype, const void* Q, int64_t q_stride_l, int64_t Lq, const void* D, int64_t d_stride_l,
+                   int64_t tok_rows, const int64_t* tok_group, const int32_t* lengths, float* scores, int64_t B,
+                   int64_t Ld_max, int64_t d, void* workspace, size_t workspace_bytes, void* stream);
+
+size_t fmx_fwd_packed_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld_max, int64_t d);
+
+int fmx_fwd_int8_packed(const void* Q, int64_t q_stride_l, int64_t Lq, const uint8_t* codes, int64_t c_stride_l,
+                        const void* scales, const void* mins, int64_t tok_rows, const int64_t* tok_group,
+                        const int32_t* lengths, float* scores, int64_t B, int64_t Ld_max, int64_t d,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+size_t fmx_fwd_int8_packed_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld_max, int64_t d);
 
 /*
  * Argmax backward of the single-query forward (argmax from fmx_fwd, Nq = 1):

@@ -119,6 +119,42 @@ def test_sparse_rejects_bad_arguments(lib):
     assert rc == FMX_ERR_INVALID and "indices" in lib.fmx_last_error().decode()
 
 
+def test_quantize_and_packed_reject_bad_arguments(lib):
+    rc = lib.fmx_quantize_int8(7, FAKE, 300 * 128, 128, 10, 300, 128, None, None, FAKE, 128, FAKE, FAKE, 300, None)
+    assert rc == FMX_ERR_INVALID and "source dtype" in lib.fmx_last_error().decode()
+    rc = lib.fmx_quantize_int8(2, FAKE, 300 * 128, 100, 10, 300, 128, None, None, FAKE, 128, FAKE, FAKE, 300, None)
+    assert rc == FMX_ERR_INVALID and "row strides" in lib.fmx_last_error().decode()
+    rc = lib.fmx_quantize_int8(2, FAKE, 300 * 128, 128, 10, 300, 128, None, None, FAKE, 128, FAKE + 1, FAKE, 300,
+                               None)
+    assert rc == FMX_ERR_INVALID and "2-byte aligned" in lib.fmx_last_error().decode()
+    assert lib.fmx_quantize_int8(2, None, 0, 128, 0, 300, 128, None, None, None, 128, None, None, 300, None) == FMX_OK
+    rc = lib.fmx_fwd_packed(0, FAKE, 128, 32, FAKE, 128, 1000, None, FAKE, FAKE, 10, 300, 128, None, 0, None)
+    assert rc == FMX_ERR_INVALID and "tok_group" in lib.fmx_last_error().decode()
+    rc = lib.fmx_fwd_int8_packed(FAKE, 128, 32, FAKE, 128, FAKE, FAKE, 1000, FAKE, None, FAKE, 10, 300, 128,
+                                 None, 0, None)
+    assert rc == FMX_ERR_INVALID and "lengths" in lib.fmx_last_error().decode()
+    assert lib.fmx_fwd_packed_workspace_bytes(10, 32, 300, 128) == 0
+    assert lib.fmx_fwd_int8_packed_workspace_bytes(10, 200, 300, 128) == 2 * 10 * 4
+
+
+def test_packed_layout_on_cpu():
+    # The packing itself is torch host logic; only scoring needs the GPU.
+    import flash_maxsim_amd as fm
+
+    D = torch.arange(6 * 9 * 8, dtype=torch.float32).reshape(6, 9, 8).half()
+    lengths = torch.tensor([9, 0, 1, 4, 5, 12])  # 12 clamps to 9
+    pk = fm.pack_docs(D, lengths)
+    assert pk.lengths.tolist() == [9, 0, 1, 4, 5, 9] and pk.max_len == 9
+    assert pk.tok_group.tolist() == [0, 3, 3, 4, 5, 7]  # exclusive prefix sum of ceil(len / 4)
+    assert pk.tokens.shape == (40, 8)
+    for b, L in enumerate(pk.lengths.tolist()):
+        r0 = 4 * pk.tok_group[b].item()
+        assert torch.equal(pk.tokens[r0:r0 + L], D[b, :L])
+        assert not pk.tokens[r0 + L:r0 + 4 * ((L + 3) // 4)].any()
+    full = fm.pack_docs(D)
+    assert full.tokens.shape == (6 * 12, 8) and full.lengths.tolist() == [9] * 6
+
+
 # ---------------------------------------------------------- Python API ----
 
 def test_python_api_asserts_like_the_reference():

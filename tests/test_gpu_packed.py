@@ -1,0 +1,143 @@
+"""GPU parity of the HIP uint8 encoder and the packed-doc forwards.
+
+quantize_int8 on a GPU tensor runs libflashmaxsim's encoder; its codes, fp16
+scales and fp16 mins must be bit-identical to the CPU oracle's restatement of
+the reference formula (oracle/maxsim_oracle.c, itself pinned to torch and to
+the golden quantiser fixture). The packed layout must hold exactly those rows,
+and the packed forwards must score like the oracle on the padded docs (1e-2,
+the north-star bar) and bit-identically to the padded GPU path, which runs the
+same kernel arithmetic on the same token rows.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import flash_maxsim_amd as fm
+from conftest import ROOT, sim, to_np32
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+ATOL = 1e-2
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy()
+
+
+def assert_quant_equal(got, want_codes, want_s, want_m):
+    codes, s, m = got
+    np.testing.assert_array_equal(codes.cpu().numpy(), want_codes)
+    np.testing.assert_array_equal(_bits(s).reshape(-1), np.asarray(want_s).view(np.int16).reshape(-1))
+    np.testing.assert_array_equal(_bits(m).reshape(-1), np.asarray(want_m).view(np.int16).reshape(-1))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("d", [128, 100, 7, 1024, 2048])
+def test_quantize_matches_oracle_bitwise(oracle_mod, dtype, d):
+    x = torch.randn(6, 37, d, generator=torch.Generator().manual_seed(d), dtype=torch.float32)
+    x[0, 0] = 0.25        # constant row: step floor 1e-8, which fp16 rounds to 0
+    x[1, 2, : d // 2] = -1.5
+    x = x.to(dtype)
+    want = oracle_mod.quantize_int8(to_np32(x))[:3]
+    got = fm.quantize_int8(x.to(DEV))
+    assert_quant_equal(got, *want)
+    # and the torch formula on the CPU (the reference's own code path)
+    t_codes, t_s, t_m = fm.quantize_int8(x)
+    np.testing.assert_array_equal(got[0].cpu().numpy(), t_codes.numpy())
+    np.testing.assert_array_equal(_bits(got[1]), _bits(t_s))
+
+
+def test_quantize_golden_fixture():
+    f = np.load(ROOT / "tests" / "golden" / "quant.npz")
+    got = fm.quantize_int8(torch.from_numpy(f["D"]).to(DEV))
+    assert_quant_equal(got, f["codes"], f["scales"], f["mins"])
+
+
+def test_quantize_strided_source(oracle_mod):
+    x = torch.randn(4, 50, 160, generator=torch.Generator().manual_seed(5)).half()
+    xs = x[:, ::2, 4:132]  # strided rows starting 8 bytes into the row: scalar path
+    want = oracle_mod.quantize_int8(to_np32(xs))[:3]
+    assert_quant_equal(fm.quantize_int8(xs.to(DEV)), *want)
+    assert_quant_equal(fm.quantize_int8(x.to(DEV)[:, ::2, 4:132]), *want)
+    assert_quant_equal(fm.quantize_int8(x.to(DEV)[:, ::2, 16:144]), *oracle_mod.quantize_int8(
+        to_np32(x[:, ::2, 16:144]))[:3])  # 16-byte aligned rows: vector path
+
+
+@pytest.mark.parametrize("d", [128, 96, 1024])
+def test_quantize_packed_layout(oracle_mod, d):
+    B, Ld = 9, 70
+    x = sim((B, Ld, d), 40 + d, torch.float32)
+    lengths = torch.tensor([70, 0, 1, 3, 4, 5, 69, 35, 80], dtype=torch.int32)  # 80 clamps to 70
+    packed = fm.quantize_int8_packed(x.to(DEV), lengths.to(DEV))
+    c_ref, s_ref, m_ref, _ = oracle_mod.quantize_int8(to_np32(x))
+    tg = packed.tok_group.cpu().numpy()
+    L = packed.lengths.cpu().numpy()
+    np.testing.assert_array_equal(L, np.clip(lengths.numpy(), 0, Ld))
+    groups = (L.astype(np.int64) + 3) // 4
+    np.testing.assert_array_equal(tg, np.cumsum(groups) - groups)
+    assert packed.codes.shape == (4 * groups.sum(), d) and packed.max_len == 70
+    codes = packed.codes.cpu().numpy()
+    sb, mb = _bits(packed.scales), _bits(packed.mins)
+    for b in range(B):
+        r0 = 4 * tg[b]
+        np.testing.assert_array_equal(codes[r0:r0 + L[b]], c_ref[b, :L[b]])
+        np.testing.assert_array_equal(sb[r0:r0 + L[b]], s_ref[b, :L[b], 0].view(np.int16))
+        np.testing.assert_array_equal(mb[r0:r0 + L[b]], m_ref[b, :L[b], 0].view(np.int16))
+        pad = slice(r0 + L[b], r0 + 4 * groups[b])
+        assert not codes[pad].any() and not sb[pad].any() and not mb[pad].any()
+
+
+@pytest.mark.parametrize("Lq, d", [(32, 128), (7, 64), (200, 128), (32, 100), (16, 512)])
+def test_int8_packed_scores(oracle_mod, Lq, d):
+    B, Ld = 40, 90
+    Q = sim((Lq, d), 60 + Lq)
+    x = sim((B, Ld, d), 61 + d, torch.float32)
+    lengths = torch.randint(0, Ld + 1, (B,), generator=torch.Generator().manual_seed(d), dtype=torch.int32)
+    lengths[:3] = torch.tensor([0, 1, Ld], dtype=torch.int32)
+    packed = fm.quantize_int8_packed(x.to(DEV), lengths.to(DEV))
+    out = fm.flash_maxsim_int8_packed(Q.to(DEV), packed)
+    codes, s16, m16, _ = oracle_mod.quantize_int8(to_np32(x))
+    ref = oracle_mod.maxsim_int8(to_np32(Q), codes, s16.astype(np.float32), m16.astype(np.float32), lengths.numpy())
+    got = out.double().cpu().numpy()
+    fin = np.isfinite(ref)
+    np.testing.assert_array_equal(np.isfinite(got), fin)
+    assert np.abs(got[fin] - ref[fin]).max() <= ATOL
+    # same kernel arithmetic as the padded layout
+    padded = fm.flash_maxsim_int8(Q.to(DEV), torch.from_numpy(codes).to(DEV), torch.from_numpy(s16).to(DEV),
+                                  torch.from_numpy(m16).to(DEV), lengths.to(DEV))
+    np.testing.assert_array_equal(out.cpu().numpy(), padded.cpu().numpy())
+
+
+@pytest.mark.parametrize("Lq, d, dtype", [(32, 128, torch.float16), (300, 128, torch.float16),
+                                          (32, 1024, torch.float16), (20, 96, torch.bfloat16)])
+def test_packed_scores(oracle_mod, Lq, d, dtype):
+    B, Ld = 30, 80
+    Q = sim((Lq, d), 70 + Lq, dtype)
+    D = sim((B, Ld, d), 71 + d, dtype)
+    lengths = torch.randint(0, Ld + 1, (B,), generator=torch.Generator().manual_seed(Lq), dtype=torch.int32)
+    lengths[0] = 0
+    packed = fm.pack_docs(D.to(DEV), lengths.to(DEV))
+    out = fm.flash_maxsim_packed(Q.to(DEV), packed)
+    ref = oracle_mod.maxsim(to_np32(Q), to_np32(D), lengths.numpy())[0]
+    got = out.double().cpu().numpy()
+    fin = np.isfinite(ref)
+    np.testing.assert_array_equal(np.isfinite(got), fin)
+    assert np.abs(got[fin] - ref[fin]).max() <= ATOL
+    padded = fm.flash_maxsim(Q.to(DEV), D.to(DEV), lengths.to(DEV))
+    np.testing.assert_array_equal(out.cpu().numpy(), padded.cpu().numpy())
+
+
+def test_packed_empty_and_all_empty(oracle_mod):
+    Q = sim((32, 128), 80)
+    D = sim((5, 16, 128), 81)
+    packed = fm.pack_docs(D.to(DEV), torch.zeros(5, dtype=torch.int32, device=DEV))
+    assert packed.tokens.shape[0] == 0
+    out = fm.flash_maxsim_packed(Q.to(DEV), packed)
+    assert torch.isneginf(out).all()
+    x = sim((3, 16, 128), 82, torch.float32)
+    pk = fm.quantize_int8_packed(x.to(DEV), torch.zeros(3, dtype=torch.int32))
+    assert torch.isneginf(fm.flash_maxsim_int8_packed(Q.to(DEV), pk)).all()
