@@ -4,10 +4,13 @@ Default workload (BASELINE metric): single-query MaxSim, Q[32,128] against
 D[5000,300,128] fp16 (reference flash_maxsim(Q, D)), inputs resident in HBM.
 A step is one flash_maxsim call over the whole batch. value = docs/s.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c1|c1_1000|c2|c3|c4|c5]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--config c1|c1_1000|c2|c3|c4|c4_packed|quant|c5|copy]
 
-The other configs are the remaining BASELINE configs, for measurement runs;
-the driver's line is the default (c1).
+The other configs are the remaining BASELINE configs (c2-c5), config 4 over
+packed docs (c4_packed), the GPU quantiser on config 4's docs (quant) and a
+device copy for counter calibration (copy), for measurement runs; the
+driver's line is the default (c1).
 
 roofline: the dominant kernel's algorithmic bytes (or flops) per launch divided
 by its average launch duration, timed with HIP events recorded on the stream
@@ -112,6 +115,52 @@ def make_workload(name):
         sn, mn, ln = scales[:200].float().numpy(), mins[:200].float().numpy(), lengths[:200].numpy()
         oracle_fn = lambda: oracle.maxsim_int8(Qn, cn, sn, mn, ln)  # noqa: E731
         return cfg, step, B, roof, oracle_fn, 200, "docs/s"
+    if name == "c4_packed":
+        # Config 4's docs (same seeds) quantised straight into the packed layout.
+        B, Lq, Ld, d = 5000, 32, 1024, 128
+        Q = sim((Lq, d), 41, torch.float16)
+        lengths = torch.randint(32, 1025, (B,), generator=torch.Generator().manual_seed(43), dtype=torch.int32)
+        Dg = torch.empty(B, Ld, d, dtype=torch.float32, device=dev)
+        for b0 in range(0, B, 500):
+            Dg[b0:b0 + 500] = sim((500, Ld, d), 42 + b0, torch.float32).to(dev)
+        packed = fm.quantize_int8_packed(Dg, lengths)
+        del Dg
+        Qd = Q.to(dev)
+        tot = int(lengths.sum())
+        cfg = {"workload": f"int8 packed varlen flash_maxsim_int8_packed Q[{Lq},{d}] x {B} docs of U[32,1024] "
+                           f"tokens, d={d} u8 ({packed.codes.shape[0]} packed rows)", "B": B, "Lq": Lq, "d": d,
+               "sum_len": tot}
+        step = lambda: fm.flash_maxsim_int8_packed(Qd, packed)  # noqa: E731
+        algo_bytes = tot * (d + 4) + Lq * d * 2 + B * 16  # + tok_group, lengths, scores
+        roof = {"bound": "hbm", "amount": algo_bytes, "unit": "GB/s", "kernel": "stream_fwd_kernel"}
+        pc = packed.codes.cpu().numpy()
+        tg, ln = packed.tok_group.cpu().numpy(), lengths.numpy()
+        ps, pm = packed.scales.float().cpu().numpy(), packed.mins.float().cpu().numpy()
+        nb = 200
+        Lmax = int(ln[:nb].max())
+        cn = np.zeros((nb, Lmax, d), np.uint8)
+        sn = np.zeros((nb, Lmax), np.float32)
+        mn = np.zeros((nb, Lmax), np.float32)
+        for b in range(nb):  # padded copies of the first docs for the CPU oracle
+            r0 = 4 * tg[b]
+            cn[b, :ln[b]], sn[b, :ln[b]], mn[b, :ln[b]] = pc[r0:r0 + ln[b]], ps[r0:r0 + ln[b]], pm[r0:r0 + ln[b]]
+        Qn, lnb = Q.float().numpy(), ln[:nb]
+        oracle_fn = lambda: oracle.maxsim_int8(Qn, cn, sn, mn, lnb)  # noqa: E731
+        return cfg, step, B, roof, oracle_fn, nb, "docs/s"
+    if name == "quant":
+        # quantize_int8 of config 4's docs on the GPU (HIP encoder), fp16 source.
+        B, Ld, d = 5000, 1024, 128
+        Dg = torch.empty(B, Ld, d, dtype=torch.float16, device=dev)
+        for b0 in range(0, B, 500):
+            Dg[b0:b0 + 500] = sim((500, Ld, d), 42 + b0, torch.float16).to(dev)
+        cfg = {"workload": f"quantize_int8 of D[{B},{Ld},{d}] fp16 -> u8 codes + fp16 scales/mins", "B": B,
+               "Ld": Ld, "d": d}
+        step = lambda: fm.quantize_int8(Dg)  # noqa: E731
+        algo_bytes = B * Ld * (d * 2 + d + 4)
+        roof = {"bound": "hbm", "amount": algo_bytes, "unit": "GB/s", "kernel": "quantize_kernel"}
+        Dn = Dg[:20].float().cpu().numpy()
+        oracle_fn = lambda: oracle.quantize_int8(Dn)  # noqa: E731
+        return cfg, step, B, roof, oracle_fn, 20, "docs/s"
     if name == "c5":
         B, Lq, Ld, d = 1000, 128, 512, 1024
         Q = sim((Lq, d), 51, torch.float16)
@@ -182,7 +231,8 @@ def main():
     # should see the clocks the GPU settles at, not that transient.
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=300)
-    ap.add_argument("--config", default="c1", help="c1 (metric), c1_1000, c2, c3, c4, c5, copy")
+    ap.add_argument("--config", default="c1",
+                    help="c1 (metric), c1_1000, c2, c3, c4, c4_packed, quant, c5, copy")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1:

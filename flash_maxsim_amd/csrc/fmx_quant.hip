@@ -9,7 +9,9 @@
 //   code = clamp(round_half_even((x - lo) / step), 0, 255)
 //   scale = fp16(step), min = fp16(lo)                (round to nearest even)
 // Every operation is a single IEEE fp32 operation in the same order, so codes,
-// scales and mins are bit-identical to the torch formula.
+// scales and mins are bit-identical to the torch formula. The quotient
+// (x - lo) / step is the correctly rounded one, computed per element from the
+// row's correctly rounded reciprocal by Markstein's correction (see div_rn).
 //
 // Output rows: token (b, j) goes to row b*Ld + j of a padded [B, Ld, d] code
 // tensor (the reference layout), or, for the packed layout, to row
@@ -69,90 +71,158 @@ __device__ __forceinline__ void load8(const void* row, int k0, int d, bool vec, 
   }
 }
 
-template <int SRC, int LPR, int CPL>
+// Correctly rounded a / b from y = RN(1 / b). q0 = RN(a * y) can be 2 ulp
+// off (y and the product each round by up to 2^-24 relative); one fma
+// correction, q1 = RN(q0 + RN(a - b*q0) * y), brings it within 1 ulp, after
+// which the remainder a - b*q1 is exact as an fma and RN(q1 + rem * y) is the
+// correctly rounded quotient (Markstein's theorem; Handbook of Floating-Point
+// Arithmetic, 2nd ed., sec. 4.7), provided nothing under- or overflows. Here
+// b >= 1e-8 and a = x - lo is 0 or >= 2^-24 for fp16 sources (a nonzero
+// difference of two fp16 values is a multiple of 2^-24); bf16/fp32 sources can
+// produce tiny nonzero a, and numerators below 2^-64 (where a remainder could
+// leave the normal range) and NaN take the IEEE division (TINY_OK = false).
+template <bool TINY_OK>
+__device__ __forceinline__ float div_rn(float a, float b, float y) {
+  if constexpr (!TINY_OK) {
+    if (!(a >= 0x1p-64f) && a != 0.f) return a / b;
+  }
+  const float q0 = a * y;
+  const float q1 = __builtin_fmaf(__builtin_fmaf(-q0, b, a), y, q0);
+  const float rem = __builtin_fmaf(-q1, b, a);
+  return __builtin_fmaf(rem, y, q1);
+}
+
+template <bool MAX>
+__device__ __forceinline__ float mm(float a, float b) {  // NaN-propagating, as torch.aminmax
+  return MAX ? __builtin_elementwise_maximum(a, b) : __builtin_elementwise_minimum(a, b);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+// Min or max over each aligned group of LPR lanes, left in every lane of the
+// group: quad permutes (lane ^ 1, lane ^ 2), then the half-row and row mirrors
+// pair quads and half-rows; groups wider than a 16-lane row use shuffles.
+template <int LPR, bool MAX>
+__device__ __forceinline__ float group_reduce(float v) {
+  if constexpr (LPR >= 2) v = mm<MAX>(v, dpp<0xB1>(v));   // quad_perm(1, 0, 3, 2)
+  if constexpr (LPR >= 4) v = mm<MAX>(v, dpp<0x4E>(v));   // quad_perm(2, 3, 0, 1)
+  if constexpr (LPR >= 8) v = mm<MAX>(v, dpp<0x141>(v));  // row_half_mirror
+  if constexpr (LPR >= 16) v = mm<MAX>(v, dpp<0x140>(v)); // row_mirror
+  if constexpr (LPR >= 32) v = mm<MAX>(v, __shfl_xor(v, 16));
+  if constexpr (LPR >= 64) v = mm<MAX>(v, __shfl_xor(v, 32));
+  return v;
+}
+
+// Each LPR-lane group takes R consecutive token rows per step and issues all
+// their loads before reducing any of them, so R rows of source are in flight
+// per group instead of one.
+template <int SRC, int LPR, int CPL, int R>
 __global__ void __launch_bounds__(256) quantize_kernel(QuantArgs a) {
-  constexpr int RPB = 256 / LPR;  // token rows per block pass
+  constexpr int GPB = 256 / LPR;  // lane groups per block
   const int lane_in_row = threadIdx.x % LPR;
   const int64_t Ld4 = (a.Ld + 3) & ~(int64_t)3;
-  const int64_t rows = a.B * Ld4;
-  for (int64_t r = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR; r < rows; r += (int64_t)gridDim.x * RPB) {
-    const int64_t b = r / Ld4, j = r - b * Ld4;
+  const bool packed = a.tok_group != nullptr;
+  // blockIdx.x: a chunk of GPB * R token rows of one doc; blockIdx.y (strided): docs.
+  const int64_t jbase = ((int64_t)blockIdx.x * GPB + threadIdx.x / LPR) * R;
+  if (jbase >= Ld4) return;
+  for (int64_t b = blockIdx.y; b < a.B; b += gridDim.y) {
     int64_t len = a.Ld;
-    if (a.lengths) {
+    if (a.lengths && packed) {  // the padded layout quantises every token
       len = a.lengths[b];
       len = len < 0 ? 0 : (len > a.Ld ? a.Ld : len);
     }
-    const bool packed = a.tok_group != nullptr;
     // Padded layout: every real token row. Packed: the first len tokens, plus
     // zero rows up to the next multiple of 4.
-    if (packed ? j >= ((len + 3) & ~(int64_t)3) : j >= a.Ld) continue;
-    const int64_t orow = packed ? 4 * a.tok_group[b] + j : b * a.Ld + j;
-    uint8_t* crow = a.codes + orow * a.c_stride_l;
-    uint16_t* sp = static_cast<uint16_t*>(a.scales) + (packed ? orow : b * a.sm_stride_b + j);
-    uint16_t* mp = static_cast<uint16_t*>(a.mins) + (packed ? orow : b * a.sm_stride_b + j);
-    if (packed && j >= len) {
-      for (int k = lane_in_row; k < a.d; k += LPR) crow[k] = 0;
-      if (lane_in_row == 0) {
-        *sp = 0;
-        *mp = 0;
+    const int64_t jend = packed ? ((len + 3) & ~(int64_t)3) : a.Ld;
+    const int64_t obase = packed ? 4 * a.tok_group[b] : b * a.Ld;
+    float x[R][CPL][8];
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      const int64_t j = jbase + k;
+      if (j < jend && j < len) {
+        const char* src = static_cast<const char*>(a.src) + (b * a.s_stride_b + j * a.s_stride_l) * a.esz;
+#pragma unroll
+        for (int cc = 0; cc < CPL; ++cc) load8<SRC>(src, (cc * LPR + lane_in_row) * 8, a.d, a.vec != 0, x[k][cc]);
       }
-      continue;
     }
-
-    const char* srow = static_cast<const char*>(a.src) + (b * a.s_stride_b + j * a.s_stride_l) * a.esz;
-    float x[CPL][8];
-    float lo = INFINITY, hi = -INFINITY;
 #pragma unroll
-    for (int cc = 0; cc < CPL; ++cc) {
-      const int k0 = (cc * LPR + lane_in_row) * 8;
-      load8<SRC>(srow, k0, a.d, a.vec != 0, x[cc]);
+    for (int k = 0; k < R; ++k) {
+      const int64_t j = jbase + k;
+      const int mode = j >= jend ? 0 : (j >= len ? 1 : 2);  // none / packed zero row / quantise
+      const int64_t orow = obase + j;
+      uint8_t* crow = a.codes + orow * a.c_stride_l;
+      const int64_t smi = packed ? orow : b * a.sm_stride_b + j;
+      uint16_t* sp = static_cast<uint16_t*>(a.scales) + smi;
+      uint16_t* mp = static_cast<uint16_t*>(a.mins) + smi;
+      if (mode == 0) continue;
+      if (mode == 1) {
+        for (int kk = lane_in_row; kk < a.d; kk += LPR) crow[kk] = 0;
+        if (lane_in_row == 0) {
+          *sp = 0;
+          *mp = 0;
+        }
+        continue;
+      }
+      float lo = INFINITY, hi = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if (k0 + i < a.d) {  // NaN-propagating, as torch.aminmax
-          lo = __builtin_elementwise_minimum(lo, x[cc][i]);
-          hi = __builtin_elementwise_maximum(hi, x[cc][i]);
+      for (int cc = 0; cc < CPL; ++cc) {
+        const int k0 = (cc * LPR + lane_in_row) * 8;
+        if (k0 + 8 <= a.d) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            lo = mm<false>(lo, x[k][cc][i]);
+            hi = mm<true>(hi, x[k][cc][i]);
+          }
+        } else {
+          for (int i = 0; i < 8 && k0 + i < a.d; ++i) {  // the row's last, partial chunk
+            lo = mm<false>(lo, x[k][cc][i]);
+            hi = mm<true>(hi, x[k][cc][i]);
+          }
         }
       }
-    }
+      lo = group_reduce<LPR, false>(lo);
+      hi = group_reduce<LPR, true>(hi);
+      float step = (hi - lo) / 255.0f;
+      if (step < 1e-8f) step = 1e-8f;  // NaN stays NaN, as torch.clamp_min
+      const float rstep = 1.0f / step;  // correctly rounded
 #pragma unroll
-    for (int s = LPR / 2; s >= 1; s >>= 1) {
-      lo = __builtin_elementwise_minimum(lo, __shfl_xor(lo, s, LPR));
-      hi = __builtin_elementwise_maximum(hi, __shfl_xor(hi, s, LPR));
-    }
-    float step = (hi - lo) / 255.0f;
-    if (step < 1e-8f) step = 1e-8f;  // NaN stays NaN, as torch.clamp_min
+      for (int cc = 0; cc < CPL; ++cc) {
+        const int k0 = (cc * LPR + lane_in_row) * 8;
+        if (k0 >= a.d) continue;
+        uint32_t w[2] = {0u, 0u};
 #pragma unroll
-    for (int cc = 0; cc < CPL; ++cc) {
-      const int k0 = (cc * LPR + lane_in_row) * 8;
-      if (k0 >= a.d) continue;
-      uint32_t w[2] = {0u, 0u};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float v = __builtin_rintf((x[cc][i] - lo) / step);
-        v = v < 0.f ? 0.f : (v > 255.f ? 255.f : v);
-        w[i >> 2] |= ((uint32_t)v & 0xffu) << (8 * (i & 3));
+        for (int i = 0; i < 8; ++i) {
+          float v = __builtin_rintf(div_rn<SRC == 0>(x[k][cc][i] - lo, step, rstep));
+          v = fminf(fmaxf(v, 0.f), 255.f);  // NaN -> 0 (fmaxf returns the number)
+          // v is an integer in [0, 255]: the byte conversion is exact.
+          w[i >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(v, i & 3, w[i >> 2]);
+        }
+        if (a.vec && k0 + 8 <= a.d) {
+          *reinterpret_cast<u32x2_t*>(crow + k0) = u32x2_t{w[0], w[1]};
+        } else {
+          for (int i = 0; i < 8 && k0 + i < a.d; ++i) crow[k0 + i] = (uint8_t)(w[i >> 2] >> (8 * (i & 3)));
+        }
       }
-      if (a.vec && k0 + 8 <= a.d) {
-        *reinterpret_cast<u32x2_t*>(crow + k0) = u32x2_t{w[0], w[1]};
-      } else {
-        for (int i = 0; i < 8 && k0 + i < a.d; ++i) crow[k0 + i] = (uint8_t)(w[i >> 2] >> (8 * (i & 3)));
+      if (lane_in_row == 0) {
+        *sp = __builtin_bit_cast(uint16_t, (_Float16)step);
+        *mp = __builtin_bit_cast(uint16_t, (_Float16)lo);
       }
-    }
-    if (lane_in_row == 0) {
-      *sp = __builtin_bit_cast(uint16_t, (_Float16)step);
-      *mp = __builtin_bit_cast(uint16_t, (_Float16)lo);
     }
   }
 }
 
 template <int SRC, int LPR, int CPL>
 hipError_t launch_q(const QuantArgs& a, hipStream_t s) {
-  constexpr int RPB = 256 / LPR;
-  const int64_t rows = a.B * ((a.Ld + 3) & ~(int64_t)3);
-  int64_t blocks = (rows + RPB - 1) / RPB;
-  if (blocks > 65536) blocks = 65536;
-  if (blocks < 1) blocks = 1;
-  hipLaunchKernelGGL((quantize_kernel<SRC, LPR, CPL>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+  constexpr int R = CPL == 1 ? 4 : (CPL == 2 ? 2 : 1);  // rows in flight per lane group
+  constexpr int RPB = 256 / LPR * R;
+  const int64_t Ld4 = (a.Ld + 3) & ~(int64_t)3;
+  const int64_t gx = (Ld4 + RPB - 1) / RPB;
+  const int64_t gy = a.B < 65535 ? a.B : 65535;
+  if (gx > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((quantize_kernel<SRC, LPR, CPL, R>), dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
