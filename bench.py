@@ -5,10 +5,11 @@ D[5000,300,128] fp16 (reference flash_maxsim(Q, D)), inputs resident in HBM.
 A step is one flash_maxsim call over the whole batch. value = docs/s.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--config c1|c1_1000|c2|c3|c4|c4_packed|quant|c5|copy]
+                    [--config c1|c1_1000|c1_topk|c2|c3|c4|c4_packed|quant|c5|copy]
 
-The other configs are the remaining BASELINE configs (c2-c5), config 4 over
-packed docs (c4_packed), the GPU quantiser on config 4's docs (quant) and a
+The other configs are the remaining BASELINE configs (c2-c5), config 1 with
+top-100 selection (c1_topk), config 4 over packed docs (c4_packed), the GPU
+quantiser on config 4's docs (quant) and a
 device copy for counter calibration (copy), for measurement runs; the
 driver's line is the default (c1).
 
@@ -67,6 +68,23 @@ def make_workload(name):
         roof = {"bound": "hbm", "amount": algo_bytes, "unit": "GB/s", "kernel": "stream_fwd_kernel"}
         Qn, Dn = Q.float().numpy(), Dh.float().numpy()
         oracle_fn = lambda: oracle.maxsim(Qn, Dn)  # noqa: E731
+        return cfg, step, B, roof, oracle_fn, B, "docs/s"
+    if name == "c1_topk":
+        # Config 1 scoring followed by top-100 selection (fused retrieval call).
+        B, Lq, Ld, d, k = 5000, 32, 300, 128, 100
+        Q = sim((Lq, d), 11, torch.float16)
+        Dh = sim((B, Ld, d), 12, torch.float16)
+        Qd, Dd = Q.to(dev), Dh.to(dev)
+        cfg = {"workload": f"flash_maxsim_topk k={k}: Q[{Lq},{d}] x D[{B},{Ld},{d}] fp16", "B": B, "Lq": Lq,
+               "Ld": Ld, "d": d, "k": k}
+        step = lambda: fm.flash_maxsim_topk(Qd, Dd, k)  # noqa: E731
+        algo_bytes = B * Ld * d * 2 + Lq * d * 2 + B * 4 * 2 + k * 12
+        roof = {"bound": "hbm", "amount": algo_bytes, "unit": "GB/s", "kernel": "stream_fwd_kernel + topk"}
+        Qn, Dn = Q.float().numpy(), Dh.float().numpy()
+
+        def oracle_fn():
+            oracle.topk(oracle.maxsim(Qn, Dn)[0], k)
+
         return cfg, step, B, roof, oracle_fn, B, "docs/s"
     if name == "c2":
         B, Lq, Ld, d = 1000, 1024, 1024, 128
@@ -232,7 +250,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--config", default="c1",
-                    help="c1 (metric), c1_1000, c2, c3, c4, c4_packed, quant, c5, copy")
+                    help="c1 (metric), c1_1000, c1_topk, c2, c3, c4, c4_packed, quant, c5, copy")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1:

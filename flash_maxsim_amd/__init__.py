@@ -6,7 +6,9 @@ signatures. ``import flash_maxsim_amd as flash_maxsim`` keeps existing call
 sites unchanged.
 
 Beyond the reference: packed variable-length docs (pack_docs,
-quantize_int8_packed, flash_maxsim_packed, flash_maxsim_int8_packed).
+quantize_int8_packed, flash_maxsim_packed, flash_maxsim_int8_packed) and
+top-k retrieval on the GPU (topk_scores, flash_maxsim_topk,
+flash_maxsim_batched_topk, flash_maxsim_int8_topk).
 """
 
 __version__ = "0.1.0"
@@ -16,6 +18,7 @@ from .flash_maxsim_quant import flash_maxsim_int8, quantize_int8, dequantize_int
 from .flash_maxsim_sparse import flash_maxsim_sparse, maxsim_sparse_naive
 from .flash_maxsim_packed import (PackedDocs, PackedInt8Docs, flash_maxsim_int8_packed, flash_maxsim_packed,
                                   pack_docs, quantize_int8_packed)
+from .flash_maxsim_topk import flash_maxsim_batched_topk, flash_maxsim_int8_topk, flash_maxsim_topk, topk_scores
 
 __all__ = [
     "flash_maxsim",
@@ -33,4 +36,8 @@ __all__ = [
     "quantize_int8_packed",
     "flash_maxsim_packed",
     "flash_maxsim_int8_packed",
+    "topk_scores",
+    "flash_maxsim_topk",
+    "flash_maxsim_batched_topk",
+    "flash_maxsim_int8_topk",
 ]

@@ -348,6 +348,40 @@ int fmx_quantize_int8(int src_dtype, const void* src, int64_t s_stride_b, int64_
   return hip_status(fmx::launch_quantize(kind, a, static_cast<hipStream_t>(stream)), "fmx_quantize_int8 launch");
 }
 
+size_t fmx_topk_workspace_bytes(int64_t Nq, int64_t B, int64_t k) {
+  if (Nq < 1 || B < 1 || k < 1 || k > FMX_MAX_TOPK) return 0;
+  return (size_t)fmx::topk_ws_keys(Nq, B, k, fmx::topk_chunk((int)k)) * sizeof(uint64_t);
+}
+
+int fmx_topk(const float* scores, int64_t s_stride_n, int64_t Nq, int64_t B, int64_t k, float* values,
+             int64_t* indices, int64_t o_stride_n, void* workspace, size_t workspace_bytes, void* stream) {
+  if (Nq < 0 || B < 0 || k < 0) return fail(FMX_ERR_INVALID, "invalid sizes Nq=%lld B=%lld k=%lld", (long long)Nq,
+                                            (long long)B, (long long)k);
+  if (k > B) return fail(FMX_ERR_INVALID, "k=%lld exceeds the %lld scores per row", (long long)k, (long long)B);
+  if (k > FMX_MAX_TOPK) return fail(FMX_ERR_UNSUPPORTED, "k=%lld exceeds FMX_MAX_TOPK=%d", (long long)k, FMX_MAX_TOPK);
+  if (B >= ((int64_t)1 << 32)) return fail(FMX_ERR_UNSUPPORTED, "B=%lld too large", (long long)B);
+  if (Nq > 65535) return fail(FMX_ERR_UNSUPPORTED, "Nq=%lld exceeds 65535 rows", (long long)Nq);
+  if (Nq == 0 || k == 0) return ok();
+  if (!scores || !values || !indices) return fail(FMX_ERR_INVALID, "scores, values and indices must be non-null");
+  if (s_stride_n < B && Nq > 1) return fail(FMX_ERR_INVALID, "score row stride %lld < B", (long long)s_stride_n);
+  if (o_stride_n < k && Nq > 1) return fail(FMX_ERR_INVALID, "output row stride %lld < k", (long long)o_stride_n);
+  const size_t need = fmx_topk_workspace_bytes(Nq, B, k);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(FMX_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) & 7u) return fail(FMX_ERR_INVALID, "workspace must be 8-byte aligned");
+  fmx::TopkArgs a = {};
+  a.scores = scores;
+  a.s_stride = s_stride_n;
+  a.Nq = Nq;
+  a.B = B;
+  a.k = (int)k;
+  a.values = values;
+  a.indices = indices;
+  a.o_stride = o_stride_n;
+  a.ws = static_cast<uint64_t*>(workspace);
+  return hip_status(fmx::launch_topk(a, static_cast<hipStream_t>(stream)), "fmx_topk launch");
+}
+
 size_t fmx_fwd_sparse_workspace_bytes(int64_t B, int64_t K, int64_t Ld, int64_t d) {
   (void)Ld;
   return stream_ws_bytes(1, B, K, d);

@@ -100,6 +100,22 @@ struct QuantArgs {
 };
 hipError_t launch_quantize(int src_kind, const QuantArgs& a, hipStream_t s);  // 0 f16, 1 bf16, 2 f32
 
+// Top-k selection over score rows (descending, NaN first, ties to the smaller
+// index).
+struct TopkArgs {
+  const float* scores;        // [Nq, B], row stride s_stride
+  int64_t s_stride;
+  int64_t Nq, B;
+  int k;                      // 1 <= k <= min(B, 1024)
+  float* values;              // [Nq, k], row stride o_stride
+  int64_t* indices;           // [Nq, k], row stride o_stride
+  int64_t o_stride;
+  uint64_t* ws;               // topk_ws_keys(Nq, B, k, topk_chunk(k)) keys
+};
+int topk_chunk(int k);                                            // keys sorted per workgroup
+int64_t topk_ws_keys(int64_t Nq, int64_t B, int64_t k, int64_t C);
+hipError_t launch_topk(const TopkArgs& a, hipStream_t s);
+
 // dQ / dD of the argmax backward.
 int bwd_dq_chunks(int B, int Lq, int d);
 size_t bwd_dd_lds_bytes(int Lq, int Ld);  // dynamic LDS of the dD kernel

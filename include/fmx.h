@@ -42,6 +42,7 @@ extern "C" {
 #define FMX_DTYPE_F32 2 /* fmx_quantize_int8 sources only */
 
 #define FMX_MAX_D 2048
+#define FMX_MAX_TOPK 1024
 
 /* Library version string ("0.1.0+mi355x"). */
 const char* fmx_version(void);
@@ -169,6 +170,23 @@ int fmx_fwd_int8_packed(const void* Q, int64_t q_stride_l, int64_t Lq, const uin
                         void* workspace, size_t workspace_bytes, void* stream);
 
 size_t fmx_fwd_int8_packed_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld_max, int64_t d);
+
+/*
+ * Top-k of score rows: for each row r < Nq of scores [Nq, B] (row stride
+ * s_stride_n), the k best (score, doc index) pairs, best first, into values
+ * [Nq, k] (fp32) and indices [Nq, k] (int64), row stride o_stride_n. Order:
+ * score descending, NaN before every number, equal scores by smaller index.
+ * 1 <= k <= min(B, FMX_MAX_TOPK); B < 2^32; Nq <= 65535.
+ *
+ * The values and the ranking are those of torch.topk(scores, k) (sorted), with
+ * ties resolved to the smaller index. No counterpart in the reference library:
+ * its callers rank flash_maxsim's scores themselves (torch topk / argsort);
+ * this is that step on the GPU, run after the scoring kernel on the same stream.
+ */
+int fmx_topk(const float* scores, int64_t s_stride_n, int64_t Nq, int64_t B, int64_t k, float* values,
+             int64_t* indices, int64_t o_stride_n, void* workspace, size_t workspace_bytes, void* stream);
+
+size_t fmx_topk_workspace_bytes(int64_t Nq, int64_t B, int64_t k);
 
 /*
  * Argmax backward of the single-query forward (argmax from fmx_fwd, Nq = 1):

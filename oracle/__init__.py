@@ -145,3 +145,25 @@ def bwd(Q, D, argmax, grad):
     dD = np.empty((B, Ld, d), dtype=np.float64)
     _load().oracle_bwd(_p(Q), _p(D), _p(am), _p(g), B, Lq, Ld, d, _p(dQ), _p(dD))
     return dQ, dD
+
+
+def topk(scores, k):
+    """(values float32 [..., k], indices int64 [..., k]) of each row's k best
+    scores: descending, NaN first (torch.topk ranks NaN above every number),
+    equal scores by smaller index. Restates the ranking callers apply to
+    flash_maxsim's output (torch topk / argsort, e.g. reference
+    benchmarks/bench.py:36, examples/demo.py:127-128) with the tie order fixed.
+    """
+    s = np.asarray(scores, dtype=np.float32)
+    rows = s.reshape(-1, s.shape[-1])
+    B = rows.shape[1]
+    idx = np.arange(B)
+    vals, inds = [], []
+    for r in rows:
+        nan = np.isnan(r)
+        neg = np.where(nan, 0.0, -r.astype(np.float64))
+        order = np.lexsort((idx, neg, ~nan))[:k]  # NaN first, then value desc, then index
+        vals.append(r[order])
+        inds.append(order.astype(np.int64))
+    shape = s.shape[:-1] + (k,)
+    return np.array(vals, dtype=np.float32).reshape(shape), np.array(inds, dtype=np.int64).reshape(shape)

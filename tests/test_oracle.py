@@ -269,3 +269,50 @@ def test_bwd_pins_reject_wrong_scatter():
         for b in range(f["D"].shape[0]):
             badQ[q] += f["grad"][b] * f["D"][b, f["argmax"][q % 2, b % 2]]
     assert not np.allclose(badQ, f["dQ"])
+
+
+# ------------------------------------------------------------------ top-k ----
+
+def _topk_scores(seed, shape):
+    g = np.random.default_rng(seed)
+    s = g.standard_normal(shape).astype(np.float32)
+    s[..., ::7] = np.round(s[..., ::7])             # many exact ties
+    s.reshape(-1)[g.integers(0, s.size, 5)] = np.nan
+    s.reshape(-1)[g.integers(0, s.size, 5)] = -np.inf
+    s.reshape(-1)[g.integers(0, s.size, 3)] = np.inf
+    return s
+
+
+@pytest.mark.parametrize("shape, k", [((50,), 10), ((3, 257), 257), ((4, 1000), 64), ((2, 31), 1)])
+def test_topk_oracle_values_are_torch_topk(oracle_mod, shape, k):
+    s = _topk_scores(k, shape)
+    v, i = oracle_mod.topk(s, k)
+    tv, ti = torch.topk(torch.from_numpy(s), k)
+    np.testing.assert_array_equal(np.nan_to_num(v, nan=7e7), np.nan_to_num(tv.numpy(), nan=7e7))
+    # every index points at its value; indices are distinct per row
+    sv = np.take_along_axis(s.reshape(-1, shape[-1]), i.reshape(-1, k), axis=1).reshape(v.shape)
+    np.testing.assert_array_equal(np.isnan(sv), np.isnan(v))
+    np.testing.assert_array_equal(sv[~np.isnan(sv)], v[~np.isnan(v)])
+    for row in i.reshape(-1, k):
+        assert len(set(row.tolist())) == k
+
+
+def test_topk_oracle_brute_force_ties(oracle_mod):
+    g = np.random.default_rng(3)
+    for trial in range(200):
+        B = int(g.integers(1, 40))
+        s = g.integers(-3, 4, B).astype(np.float32)   # dense ties
+        if trial % 5 == 0:
+            s[g.integers(0, B)] = np.nan
+        k = int(g.integers(1, B + 1))
+        want = sorted(range(B), key=lambda j: (0 if np.isnan(s[j]) else 1, 0.0 if np.isnan(s[j]) else -s[j], j))[:k]
+        v, i = oracle_mod.topk(s, k)
+        assert i.tolist() == want
+
+
+def test_topk_oracle_planted_mistake_fails(oracle_mod):
+    # a last-index tie order (as a sort that is not stable could give) must differ
+    s = np.array([2.0, 5.0, 2.0, 5.0, 2.0], np.float32)
+    _, i = oracle_mod.topk(s, 5)
+    assert i.tolist() == [1, 3, 0, 2, 4]
+    assert i.tolist() != [3, 1, 4, 2, 0]
