@@ -8,12 +8,15 @@ sites unchanged.
 Beyond the reference: packed variable-length docs (pack_docs,
 quantize_int8_packed, flash_maxsim_packed, flash_maxsim_int8_packed) and
 top-k retrieval on the GPU (topk_scores, flash_maxsim_topk,
-flash_maxsim_batched_topk, flash_maxsim_int8_topk).
+flash_maxsim_batched_topk, flash_maxsim_int8_topk), and training with doc
+lengths (flash_maxsim_train's doc_lengths) or several queries
+(flash_maxsim_train_batched).
 """
 
 __version__ = "0.1.0"
 
-from .flash_maxsim import flash_maxsim, flash_maxsim_batched, flash_maxsim_train, maxsim_naive
+from .flash_maxsim import (flash_maxsim, flash_maxsim_batched, flash_maxsim_train, flash_maxsim_train_batched,
+                           maxsim_naive)
 from .flash_maxsim_quant import flash_maxsim_int8, quantize_int8, dequantize_int8
 from .flash_maxsim_sparse import flash_maxsim_sparse, maxsim_sparse_naive
 from .flash_maxsim_packed import (PackedDocs, PackedInt8Docs, flash_maxsim_int8_packed, flash_maxsim_packed,
@@ -40,4 +43,5 @@ __all__ = [
     "flash_maxsim_topk",
     "flash_maxsim_batched_topk",
     "flash_maxsim_int8_topk",
+    "flash_maxsim_train_batched",
 ]

@@ -67,6 +67,12 @@ _SIGNATURES = {
          _i64, _i64, _i64, _i64, _ptr, _size, _ptr],
     ),
     "fmx_bwd_workspace_bytes": (_size, [_i64, _i64, _i64, _i64]),
+    "fmx_bwd_batched": (
+        _int,
+        [_int, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _ptr,
+         _i64, _i64, _i64, _i64, _i64, _ptr, _size, _ptr],
+    ),
+    "fmx_bwd_batched_workspace_bytes": (_size, [_i64, _i64, _i64, _i64, _i64]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

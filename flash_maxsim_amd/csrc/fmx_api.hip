@@ -433,48 +433,76 @@ int fmx_fwd_sparse(int dtype, const void* Q, int64_t q_stride_l, int64_t Lq, con
   return hip_status(e, "fmx_fwd_sparse launch");
 }
 
-size_t fmx_bwd_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld, int64_t d) {
+size_t fmx_bwd_batched_workspace_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t Ld, int64_t d) {
   (void)Ld;
-  if (B < 0 || Lq < 1 || d < 1) return 0;
-  return (size_t)fmx::bwd_dq_chunks((int)B, (int)Lq, (int)d) * (size_t)Lq * (size_t)d * sizeof(float);
+  if (Nq < 1 || B < 0 || Lq < 1 || d < 1 || Nq * Lq > INT32_MAX) return 0;
+  const int64_t rows = Nq * Lq;
+  return (size_t)fmx::bwd_dq_chunks((int)B, (int)rows, (int)d) * (size_t)rows * (size_t)d * sizeof(float);
 }
 
-int fmx_bwd(int dtype, const void* Q, int64_t q_stride_l, const void* D, int64_t d_stride_b,
-            int64_t d_stride_l, const int32_t* argmax, const float* grad_scores, void* dQ, void* dD,
-            int64_t B, int64_t Lq, int64_t Ld, int64_t d, void* workspace, size_t workspace_bytes,
-            void* stream) {
+size_t fmx_bwd_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld, int64_t d) {
+  return fmx_bwd_batched_workspace_bytes(1, B, Lq, Ld, d);
+}
+
+int fmx_bwd_batched(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, const void* D,
+                    int64_t d_stride_b, int64_t d_stride_l, const int32_t* lengths, const int32_t* argmax,
+                    const float* grad_scores, int64_t g_stride_n, int64_t g_stride_b, void* dQ, void* dD,
+                    int64_t Nq, int64_t B, int64_t Lq, int64_t Ld, int64_t d, void* workspace,
+                    size_t workspace_bytes, void* stream) {
   if (dtype != FMX_DTYPE_F16 && dtype != FMX_DTYPE_BF16) return fail(FMX_ERR_INVALID, "unknown dtype %d", dtype);
-  int rc = check_common(1, B, Lq, Ld, d, q_stride_l, d_stride_b, d_stride_l, 2);
+  int rc = check_common(Nq, B, Lq, Ld, d, q_stride_l, d_stride_b, d_stride_l, 2);
   if (rc) return rc;
   if (Ld < 1) return fail(FMX_ERR_INVALID, "backward needs Ld >= 1");
+  if (g_stride_n < 0 || g_stride_b < 0) return fail(FMX_ERR_INVALID, "gradient strides must be >= 0");
   if (!dQ && !dD) return ok();
-  if (!Q || !D || !argmax || !grad_scores) return fail(FMX_ERR_INVALID, "Q, D, argmax and grad must be non-null");
+  if (!Q || !D || (B > 0 && (!argmax || !grad_scores))) return fail(FMX_ERR_INVALID, "Q, D, argmax and grad must be non-null");
   if (!aligned16(Q) || !aligned16(D)) return fail(FMX_ERR_INVALID, "Q and D must be 16-byte aligned");
   if ((dQ && !aligned16(dQ)) || (dD && !aligned16(dD))) return fail(FMX_ERR_INVALID, "dQ and dD must be 16-byte aligned");
-  if (fmx::bwd_dd_lds_bytes((int)Lq, (int)Ld) > 64 * 1024)
-    return fail(FMX_ERR_UNSUPPORTED, "Lq=%lld, Ld=%lld exceed the dD kernel's LDS", (long long)Lq, (long long)Ld);
-  const size_t need = fmx_bwd_workspace_bytes(B, Lq, Ld, d);
+  if (Nq > 1 && (q_stride_n & 7)) return fail(FMX_ERR_INVALID, "Q query stride must be a multiple of 8");
+  if (dD) {
+    if (Nq * Lq >= 8192 || Ld >= (1 << 19))
+      return fail(FMX_ERR_UNSUPPORTED, "dD kernel covers Nq*Lq < 8192 and Ld < 2^19 (Nq*Lq=%lld, Ld=%lld)",
+                  (long long)(Nq * Lq), (long long)Ld);
+    if (fmx::bwd_dd_lds_bytes(Nq * Lq, Ld) > 64 * 1024)
+      return fail(FMX_ERR_UNSUPPORTED, "Nq*Lq=%lld, Ld=%lld exceed the dD kernel's LDS", (long long)(Nq * Lq),
+                  (long long)Ld);
+  }
+  const size_t need = fmx_bwd_batched_workspace_bytes(Nq, B, Lq, Ld, d);
   if (dQ && (!workspace || workspace_bytes < need))
     return fail(FMX_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
 
   fmx::BwdArgs a = {};
   a.Q = Q;
   a.D = D;
+  a.lengths = lengths;
   a.argmax = argmax;
   a.grad = grad_scores;
   a.dQ = dQ;
   a.dD = dD;
   a.ws = static_cast<float*>(workspace);
+  a.sq_n = Nq > 1 ? q_stride_n : 0;
   a.sq_l = q_stride_l;
   a.sd_b = d_stride_b;
   a.sd_l = d_stride_l;
+  a.g_n = g_stride_n;
+  a.g_b = g_stride_b;
+  a.Nq = (int)Nq;
   a.B = (int)B;
   a.Lq = (int)Lq;
   a.Ld = (int)Ld;
   a.d = (int)d;
-  a.nchunk = fmx::bwd_dq_chunks((int)B, (int)Lq, (int)d);
+  a.nchunk = fmx::bwd_dq_chunks((int)B, (int)(Nq * Lq), (int)d);
+  a.sort_n = fmx::bwd_sort_n(Nq * Lq);
   const int kind = dtype == FMX_DTYPE_BF16 ? fmx::KIND_BF16 : fmx::KIND_F16;
   return hip_status(fmx::launch_bwd(kind, a, static_cast<hipStream_t>(stream)), "fmx_bwd launch");
+}
+
+int fmx_bwd(int dtype, const void* Q, int64_t q_stride_l, const void* D, int64_t d_stride_b,
+            int64_t d_stride_l, const int32_t* argmax, const float* grad_scores, void* dQ, void* dD,
+            int64_t B, int64_t Lq, int64_t Ld, int64_t d, void* workspace, size_t workspace_bytes,
+            void* stream) {
+  return fmx_bwd_batched(dtype, Q, 0, q_stride_l, D, d_stride_b, d_stride_l, nullptr, argmax, grad_scores, 0, 1,
+                         dQ, dD, 1, B, Lq, Ld, d, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

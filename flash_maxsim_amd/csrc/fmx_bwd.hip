@@ -1,17 +1,20 @@
-// Argmax backward of single-query MaxSim.
+// Argmax backward of MaxSim (single or batched queries over shared docs).
 //
 // Replaces _maxsim_bwd_dQ_kernel and _maxsim_bwd_dD_kernel (reference
-// flash_maxsim/flash_maxsim.py:153-188) with the same mathematics:
-//   dQ[q, :]    = sum_b g[b] * D[b, a[b, q], :]
-//   dD[b, j, :] = g[b] * sum_{q : a[b, q] = j} Q[q, :]
+// flash_maxsim/flash_maxsim.py:153-188) with the same mathematics, extended to
+// Nq queries and doc lengths (a = argmax, g = upstream gradient of scores):
+//   dQ[qi, q, :] = sum_b g[qi, b] * D[b, a[qi*B + b, q], :]
+//   dD[b, j, :]  = sum_{(qi, q) : a[qi*B + b, q] = j} g[qi, b] * Q[qi, q, :]
+// Docs of length 0 (every similarity masked, score -inf) take no part, as in
+// autograd through the masked naive MaxSim.
 // Differences by design:
 //  * dQ is a two-stage gather-reduce: doc chunks accumulate fp32 partials in a
 //    caller workspace, then a second kernel adds the chunks in order. The
 //    reference runs one program per query token looping over every doc.
 //  * dD is written exactly once per element by the doc's workgroup (zeros for
-//    rows no query token picked, the fp32 sum for picked rows), so there is no
-//    torch.zeros_like memset and no fp16 atomics; results are bitwise
-//    deterministic.
+//    rows no query token picked, the fp32 sum for picked rows, in (query,
+//    token) order), so there is no torch.zeros_like memset and no fp16
+//    atomics; results are bitwise deterministic.
 #include "fmx_device.h"
 #include "fmx_kernels.h"
 
@@ -74,39 +77,51 @@ __device__ __forceinline__ void store8(uint16_t* row, int k0, int d, const float
 
 __device__ __forceinline__ int clamp_index(int j, int Ld) { return j < 0 ? 0 : (j >= Ld ? Ld - 1 : j); }
 
-// Stage 1 of dQ: one thread per (query token q, 8-wide k chunk), one grid row
-// per chunk of docs; ws[chunk][q][k] = sum over the chunk's docs, in order.
+__device__ __forceinline__ int doc_len(const BwdArgs& a, int b) {
+  if (!a.lengths) return a.Ld;
+  const int l = a.lengths[b];
+  return l < 0 ? 0 : (l > a.Ld ? a.Ld : l);
+}
+
+// Stage 1 of dQ: one thread per (query token row r = qi*Lq + q, 8-wide k
+// chunk), one grid row per chunk of docs; ws[chunk][r][k] = sum over the
+// chunk's docs, in order.
 template <bool BF>
 __global__ void __launch_bounds__(256) bwd_dq_partial_kernel(BwdArgs a) {
   const int nkc = (a.d + 7) >> 3;
+  const int64_t rows = (int64_t)a.Nq * a.Lq;
   const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (tid >= (int64_t)a.Lq * nkc) return;
-  const int q = (int)(tid / nkc);
-  const int k0 = (int)(tid - (int64_t)q * nkc) * 8;
+  if (tid >= rows * nkc) return;
+  const int64_t r = tid / nkc;
+  const int k0 = (int)(tid - r * nkc) * 8;
+  const int qi = (int)(r / a.Lq), q = (int)(r - (int64_t)qi * a.Lq);
   const int per = (a.B + a.nchunk - 1) / a.nchunk;
   const int b0 = blockIdx.y * per;
   const int b1 = min(a.B, b0 + per);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   const uint16_t* D = static_cast<const uint16_t*>(a.D);
+  const int32_t* am = a.argmax + (int64_t)qi * a.B * a.Lq + q;
+  const float* g = a.grad + (int64_t)qi * a.g_n;
 #pragma unroll 4
   for (int b = b0; b < b1; ++b) {
-    const int j = clamp_index(a.argmax[(int64_t)b * a.Lq + q], a.Ld);
-    const float gb = a.grad[b];
+    if (a.lengths && doc_len(a, b) == 0) continue;
+    const int j = clamp_index(am[(int64_t)b * a.Lq], a.Ld);
+    const float gb = g[(int64_t)b * a.g_b];
     float x[8];
     load8<BF>(D + (int64_t)b * a.sd_b + (int64_t)j * a.sd_l, k0, a.d, x);
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] = fmaf(gb, x[e], acc[e]);
   }
-  float* out = a.ws + ((int64_t)blockIdx.y * a.Lq + q) * a.d + k0;
+  float* out = a.ws + ((int64_t)blockIdx.y * rows + r) * a.d + k0;
 #pragma unroll
   for (int e = 0; e < 8; ++e)
     if (k0 + e < a.d) out[e] = acc[e];
 }
 
-// Stage 2 of dQ: dQ[q][k] = sum over chunks (in order) of ws[chunk][q][k].
+// Stage 2 of dQ: dQ[r][k] = sum over chunks (in order) of ws[chunk][r][k].
 template <bool BF>
 __global__ void __launch_bounds__(256) bwd_dq_finalize_kernel(BwdArgs a) {
-  const int64_t n = (int64_t)a.Lq * a.d;
+  const int64_t n = (int64_t)a.Nq * a.Lq * a.d;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
   float s = 0.f;
@@ -114,33 +129,50 @@ __global__ void __launch_bounds__(256) bwd_dq_finalize_kernel(BwdArgs a) {
   static_cast<uint16_t*>(a.dQ)[i] = Elem<BF>::from_f(s);
 }
 
-// dD for one doc per workgroup. LDS: argmax row, query tokens sorted by
-// (row, token), and a bitmap of rows picked by some token.
+constexpr int kEntryBits = 13;  // (query, token) entries per doc < 2^13
+
+// dD for one doc per workgroup. LDS: the doc's (query, token) entries as keys
+// row << 13 | entry, sorted ascending (bitonic), and a bitmap of picked rows.
+// A picked row's entries are then contiguous and in entry order.
 template <bool BF>
 __global__ void __launch_bounds__(256) bwd_dd_kernel(BwdArgs a) {
-  extern __shared__ int smem[];
-  int* am = smem;
-  int* order = smem + a.Lq;
-  uint32_t* hit = reinterpret_cast<uint32_t*>(smem + 2 * a.Lq);
+  extern __shared__ uint32_t smem[];
+  uint32_t* keys = smem;
+  uint32_t* hit = smem + a.sort_n;
   const int b = blockIdx.x;
+  const int nkc = (a.d + 7) >> 3;
+  const int NL = a.Nq * a.Lq;
+  const bool empty = a.lengths && doc_len(a, b) == 0;
   const int nwords = (a.Ld + 31) >> 5;
   for (int i = threadIdx.x; i < nwords; i += 256) hit[i] = 0u;
-  for (int q = threadIdx.x; q < a.Lq; q += 256) am[q] = clamp_index(a.argmax[(int64_t)b * a.Lq + q], a.Ld);
   __syncthreads();
-  for (int q = threadIdx.x; q < a.Lq; q += 256) {
-    const int j = am[q];
-    atomicOr(&hit[j >> 5], 1u << (j & 31));
-    int rank = 0;
-    for (int q2 = 0; q2 < a.Lq; ++q2) {
-      const int j2 = am[q2];
-      rank += (j2 < j) || (j2 == j && q2 < q);
+  for (int e = threadIdx.x; e < a.sort_n; e += 256) {
+    uint32_t key = 0xffffffffu;
+    if (e < NL && !empty) {
+      const int qi = e / a.Lq, q = e - qi * a.Lq;
+      const int j = clamp_index(a.argmax[((int64_t)qi * a.B + b) * a.Lq + q], a.Ld);
+      key = ((uint32_t)j << kEntryBits) | (uint32_t)e;
+      atomicOr(&hit[j >> 5], 1u << (j & 31));
     }
-    order[rank] = q;
+    keys[e] = key;
   }
   __syncthreads();
+  for (int size = 2; size <= a.sort_n; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int p = threadIdx.x; p < a.sort_n / 2; p += 256) {
+        const int i = 2 * stride * (p / stride) + (p % stride);
+        const int j = i + stride;
+        const bool asc = (i & size) == 0;
+        const uint32_t x = keys[i], y = keys[j];
+        if ((x > y) == asc) {
+          keys[i] = y;
+          keys[j] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
 
-  const float gb = a.grad[b];
-  const int nkc = (a.d + 7) >> 3;
   uint16_t* out = static_cast<uint16_t*>(a.dD) + (int64_t)b * a.Ld * a.d;
   const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   const int64_t zn = (int64_t)a.Ld * nkc;
@@ -149,22 +181,24 @@ __global__ void __launch_bounds__(256) bwd_dd_kernel(BwdArgs a) {
     const int k0 = (int)(e - (int64_t)row * nkc) * 8;
     if (!((hit[row >> 5] >> (row & 31)) & 1u)) store8<BF>(out + (int64_t)row * a.d, k0, a.d, zero);
   }
+  if (empty) return;
   const uint16_t* Q = static_cast<const uint16_t*>(a.Q);
-  const int64_t hn = (int64_t)a.Lq * nkc;
-  for (int64_t e = threadIdx.x; e < hn; e += 256) {
-    const int p = (int)(e / nkc);
-    const int k0 = (int)(e - (int64_t)p * nkc) * 8;
-    const int j = am[order[p]];
-    if (p > 0 && am[order[p - 1]] == j) continue;  // not the first token of its row group
+  const int64_t hn = (int64_t)NL * nkc;
+  for (int64_t w = threadIdx.x; w < hn; w += 256) {
+    const int p = (int)(w / nkc);
+    const int k0 = (int)(w - (int64_t)p * nkc) * 8;
+    const uint32_t j = keys[p] >> kEntryBits;
+    if (p > 0 && (keys[p - 1] >> kEntryBits) == j) continue;  // not the first entry of its row
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int p2 = p; p2 < a.Lq && am[order[p2]] == j; ++p2) {
+    for (int p2 = p; p2 < NL && (keys[p2] >> kEntryBits) == j; ++p2) {
+      const int e = (int)(keys[p2] & ((1u << kEntryBits) - 1));
+      const int qi = e / a.Lq, q = e - qi * a.Lq;
+      const float g = a.grad[(int64_t)qi * a.g_n + (int64_t)b * a.g_b];
       float x[8];
-      load8<BF>(Q + (int64_t)order[p2] * a.sq_l, k0, a.d, x);
+      load8<BF>(Q + (int64_t)qi * a.sq_n + (int64_t)q * a.sq_l, k0, a.d, x);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) acc[k] += x[k];
+      for (int k = 0; k < 8; ++k) acc[k] = fmaf(g, x[k], acc[k]);
     }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) acc[k] *= gb;
     store8<BF>(out + (int64_t)j * a.d, k0, a.d, acc);
   }
 }
@@ -173,14 +207,14 @@ template <bool BF>
 hipError_t launch_bwd_t(const BwdArgs& a, hipStream_t s) {
   const int nkc = (a.d + 7) >> 3;
   if (a.dQ) {
-    const int64_t threads = (int64_t)a.Lq * nkc;
+    const int64_t threads = (int64_t)a.Nq * a.Lq * nkc;
     hipLaunchKernelGGL(bwd_dq_partial_kernel<BF>, dim3((unsigned)((threads + 255) / 256), a.nchunk), dim3(256),
                        0, s, a);
-    const int64_t n = (int64_t)a.Lq * a.d;
+    const int64_t n = (int64_t)a.Nq * a.Lq * a.d;
     hipLaunchKernelGGL(bwd_dq_finalize_kernel<BF>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
   }
   if (a.dD && a.B > 0) {
-    const size_t lds = (size_t)(2 * a.Lq + (a.Ld + 31) / 32) * sizeof(int);
+    const size_t lds = bwd_dd_lds_bytes((int64_t)a.Nq * a.Lq, a.Ld);
     hipLaunchKernelGGL(bwd_dd_kernel<BF>, dim3((unsigned)a.B), dim3(256), lds, s, a);
   }
   return hipGetLastError();
@@ -188,11 +222,11 @@ hipError_t launch_bwd_t(const BwdArgs& a, hipStream_t s) {
 
 }  // namespace
 
-// Doc chunks of the dQ gather: enough (q, k-chunk, doc-chunk) threads to keep
+// Doc chunks of the dQ gather: enough (row, k-chunk, doc-chunk) threads to keep
 // the GPU's loads in flight (about 2^19), at most 64 chunks, at least 8 docs each.
-int bwd_dq_chunks(int B, int Lq, int d) {
+int bwd_dq_chunks(int B, int rows, int d) {
   if (B <= 0) return 1;
-  const int64_t per_chunk = (int64_t)Lq * ((d + 7) / 8);
+  const int64_t per_chunk = (int64_t)rows * ((d + 7) / 8);
   int64_t n = ((int64_t)1 << 19) / (per_chunk > 0 ? per_chunk : 1);
   const int64_t by_docs = (B + 7) / 8;
   if (n > by_docs) n = by_docs;
@@ -201,7 +235,15 @@ int bwd_dq_chunks(int B, int Lq, int d) {
   return (int)n;
 }
 
-size_t bwd_dd_lds_bytes(int Lq, int Ld) { return (size_t)(2 * Lq + (Ld + 31) / 32) * sizeof(int); }
+int bwd_sort_n(int64_t entries) {
+  int n = 64;
+  while (n < entries) n <<= 1;
+  return n;
+}
+
+size_t bwd_dd_lds_bytes(int64_t entries, int64_t Ld) {
+  return ((size_t)bwd_sort_n(entries) + (size_t)((Ld + 31) / 32)) * sizeof(uint32_t);
+}
 
 hipError_t launch_bwd(int kind, const BwdArgs& a, hipStream_t s) {
   switch (kind) {

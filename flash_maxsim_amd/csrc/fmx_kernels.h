@@ -35,18 +35,20 @@ struct FwdArgs {
                               // readable 4 tokens per 8-byte load (compile-time path)
 };
 
-// Backward of the single-query forward with saved argmax.
+// Backward of the forward with saved argmax (Nq queries, shared docs).
 struct BwdArgs {
-  const void* Q;              // [Lq, d], row stride sq_l
+  const void* Q;              // [Nq, Lq, d], strides sq_n, sq_l
   const void* D;              // [B, Ld, d], strides sd_b, sd_l
-  const int32_t* argmax;      // [B, Lq]
-  const float* grad;          // [B]
-  void* dQ;                   // [Lq, d] contiguous, or null
+  const int32_t* lengths;     // [B] or null: docs of length <= 0 get and give no gradient
+  const int32_t* argmax;      // [Nq*B, Lq], row qi*B + b
+  const float* grad;          // [Nq, B], strides g_n, g_b (either may be 0)
+  void* dQ;                   // [Nq, Lq, d] contiguous, or null
   void* dD;                   // [B, Ld, d] contiguous, or null
-  float* ws;                  // dQ partial sums [nchunk, Lq, d]
-  int64_t sq_l, sd_b, sd_l;
-  int B, Lq, Ld, d;
+  float* ws;                  // dQ partial sums [nchunk, Nq*Lq, d]
+  int64_t sq_n, sq_l, sd_b, sd_l, g_n, g_b;
+  int Nq, B, Lq, Ld, d;
   int nchunk;                 // doc chunks of the dQ gather
+  int sort_n;                 // dD: (query, token) entries per doc padded to a power of two
 };
 
 // Shape class handled by the streaming kernel (query tile in VGPRs, docs read
@@ -117,8 +119,9 @@ int64_t topk_ws_keys(int64_t Nq, int64_t B, int64_t k, int64_t C);
 hipError_t launch_topk(const TopkArgs& a, hipStream_t s);
 
 // dQ / dD of the argmax backward.
-int bwd_dq_chunks(int B, int Lq, int d);
-size_t bwd_dd_lds_bytes(int Lq, int Ld);  // dynamic LDS of the dD kernel
+int bwd_dq_chunks(int B, int rows, int d);     // rows = Nq * Lq query tokens
+int bwd_sort_n(int64_t entries);               // power of two >= Nq * Lq (>= 64)
+size_t bwd_dd_lds_bytes(int64_t entries, int64_t Ld);  // dynamic LDS of the dD kernel
 hipError_t launch_bwd(int kind, const BwdArgs& a, hipStream_t s);
 
 }  // namespace fmx

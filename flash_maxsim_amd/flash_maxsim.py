@@ -140,63 +140,84 @@ def flash_maxsim_batched(Q: torch.Tensor, D: torch.Tensor, doc_lengths=None,
 
 
 class _FlashMaxSimFn(torch.autograd.Function):
-    """Autograd node of flash_maxsim_train (reference flash_maxsim.py:253-286).
+    """Autograd node of flash_maxsim_train / flash_maxsim_train_batched
+    (reference flash_maxsim.py:253-286, extended to Nq queries and doc lengths).
 
-    The forward kernel records, for every (doc, query token), the first doc
-    token reaching the max; the gradient of a max flows only to that token, so
-    the backward is a gather (dQ) and a scatter (dD) through those indices.
+    The forward kernel records, for every (query, doc, query token), the first
+    doc token reaching the max; the gradient of a max flows only to that token,
+    so the backward is a gather (dQ) and a scatter (dD) through those indices.
+    Docs of length 0 score -inf and get and give no gradient, as in autograd
+    through maxsim_naive.
     """
 
     @staticmethod
-    def forward(ctx, Q, D):
-        Lq, d = Q.shape
+    def forward(ctx, Q, D, lengths):
+        batched = Q.ndim == 3
+        Q3 = Q if batched else Q.unsqueeze(0)
+        Nq, Lq, d = Q3.shape
         B, Ld = D.shape[:2]
         kdt = _kernel_dtype(Q, D)
-        Qk, Dk = _prep(Q, kdt), _prep(D, kdt)
-        scores, argmax = _launch_fwd(Qk.unsqueeze(0), Dk, None, 1, B, Lq, Ld, d, True, True)
-        ctx.save_for_backward(Qk, Dk, argmax)
+        Qk, Dk = _prep(Q3, kdt), _prep(D, kdt)
+        scores, argmax = _launch_fwd(Qk, Dk, lengths, Nq, B, Lq, Ld, d, True, True)
+        ctx.save_for_backward(Qk, Dk, argmax, lengths)
         ctx.d = d
-        return scores[0]
+        ctx.batched = batched
+        return scores if batched else scores[0]
 
     @staticmethod
     def backward(ctx, grad_scores):
-        Qk, Dk, argmax = ctx.saved_tensors
+        Qk, Dk, argmax, lengths = ctx.saved_tensors
         d = ctx.d
-        Lq = Qk.shape[0]
+        Nq, Lq = Qk.shape[:2]
         B, Ld = Dk.shape[:2]
         need_q, need_d = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         dev = _check_devices(Qk, Dk, grad_scores)
-        grad_Q = torch.empty(Lq, d, device=dev, dtype=Qk.dtype) if need_q else None
+        grad_Q = torch.empty(Nq, Lq, d, device=dev, dtype=Qk.dtype) if need_q else None
         grad_D = torch.empty(B, Ld, d, device=dev, dtype=Dk.dtype) if need_d else None
-        if (grad_Q is None and grad_D is None) or Lq == 0:
+        if (grad_Q is None and grad_D is None) or Lq == 0 or Ld == 0 or B == 0:
             if grad_Q is not None:
                 grad_Q.zero_()
             if grad_D is not None:
                 grad_D.zero_()
-            return grad_Q, grad_D
-        g = grad_scores.contiguous().float()
-        lib = _lib.load()
-        nbytes = lib.fmx_bwd_workspace_bytes(B, Lq, Ld, d) if need_q else 0
-        ws = _lib.workspace(nbytes, dev)
-        with _device_guard(dev):
-            rc = lib.fmx_bwd(
-                _lib.dtype_code(Qk), Qk.data_ptr(), Qk.stride(0), Dk.data_ptr(), Dk.stride(0), Dk.stride(1),
-                argmax.data_ptr(), g.data_ptr(), _lib.ptr(grad_Q), _lib.ptr(grad_D),
-                B, Lq, Ld, d, _lib.ptr(ws), nbytes, _lib.stream_of(Qk),
-            )
-        _lib.check(rc)
-        return grad_Q, grad_D
+        else:
+            # fp32 gradient read in place through its strides (the expanded
+            # gradient of scores.sum() has stride 0: no copy).
+            g = grad_scores.float().reshape(Nq, B) if not ctx.batched else grad_scores.float()
+            if g.dim() == 1:
+                g = g.unsqueeze(0)
+            lib = _lib.load()
+            nbytes = lib.fmx_bwd_batched_workspace_bytes(Nq, B, Lq, Ld, d) if need_q else 0
+            ws = _lib.workspace(nbytes, dev)
+            with _device_guard(dev):
+                rc = lib.fmx_bwd_batched(
+                    _lib.dtype_code(Qk), Qk.data_ptr(), Qk.stride(0), Qk.stride(1), Dk.data_ptr(), Dk.stride(0),
+                    Dk.stride(1), _lib.ptr(lengths), argmax.data_ptr(), g.data_ptr(), g.stride(0), g.stride(1),
+                    _lib.ptr(grad_Q), _lib.ptr(grad_D), Nq, B, Lq, Ld, d, _lib.ptr(ws), nbytes, _lib.stream_of(Qk),
+                )
+            _lib.check(rc)
+        if grad_Q is not None and not ctx.batched:
+            grad_Q = grad_Q[0]
+        return grad_Q, grad_D, None
 
 
-def flash_maxsim_train(Q: torch.Tensor, D: torch.Tensor) -> torch.Tensor:
-    """flash_maxsim over full-length docs, differentiable in Q and D: float32 [B].
+def flash_maxsim_train(Q: torch.Tensor, D: torch.Tensor, doc_lengths=None) -> torch.Tensor:
+    """flash_maxsim differentiable in Q and D: float32 [B].
 
     Gradients come back in the kernel dtype (fp16, or bf16 for bf16 inputs);
     autograd casts them to the leaves' dtypes. Reference signature:
-    flash_maxsim.py:289.
+    flash_maxsim.py:289 (Q, D); doc_lengths is an extension (the reference
+    trains on full-length docs only, :260).
     """
     assert Q.ndim == 2 and D.ndim == 3 and Q.size(1) == D.size(2)
-    return _FlashMaxSimFn.apply(Q, D)
+    return _FlashMaxSimFn.apply(Q, D, _lengths(D.size(0), D.device, doc_lengths))
+
+
+def flash_maxsim_train_batched(Q: torch.Tensor, D: torch.Tensor, doc_lengths=None) -> torch.Tensor:
+    """Nq queries against shared docs, differentiable in Q and D: float32
+    [Nq, B] (the scores of flash_maxsim_batched with shared_docs=True).
+    Extension: the reference trains one query at a time (flash_maxsim.py:289)."""
+    assert Q.ndim == 3 and D.ndim == 3 and Q.size(2) == D.size(2)
+    return _FlashMaxSimFn.apply(Q, D, _lengths(D.size(0), D.device, doc_lengths))
 
 
 def maxsim_naive(Q: torch.Tensor, D: torch.Tensor, doc_lengths=None) -> torch.Tensor:

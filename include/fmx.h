@@ -206,6 +206,31 @@ int fmx_bwd(int dtype, const void* Q, int64_t q_stride_l, const void* D, int64_t
 
 size_t fmx_bwd_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld, int64_t d);
 
+/*
+ * Argmax backward of the batched forward (argmax from fmx_fwd with Nq >= 1,
+ * shared docs), with doc lengths:
+ *   dQ[qi, q, :] = sum_b g[qi, b] * D[b, argmax[qi*B + b, q], :]
+ *   dD[b, j, :]  = sum_{(qi, q) : argmax[qi*B + b, q] = j} g[qi, b] * Q[qi, q, :]
+ * where g = grad_scores [Nq, B] with strides (g_stride_n, g_stride_b), either
+ * of which may be 0 (an expanded gradient, such as that of scores.sum(), is
+ * read in place). Docs with lengths[b] <= 0 (score -inf) take no part, as in
+ * autograd through the masked naive MaxSim; lengths may be NULL (= Ld).
+ * dQ [Nq, Lq, d] and dD [B, Ld, d] are written contiguous in `dtype`, each
+ * skipped when NULL; dD rows no token picked are zeros, picked rows are the
+ * fp32 sum in (qi, q) order (deterministic). dD needs Nq*Lq < 8192, Ld < 2^19.
+ *
+ * Generalises fmx_bwd (which is its Nq = 1, lengths = NULL case; reference
+ * flash_maxsim/flash_maxsim.py:265-286) to the batched and variable-length
+ * training the reference's flash_maxsim_train does not offer (:289-291).
+ */
+int fmx_bwd_batched(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, const void* D,
+                    int64_t d_stride_b, int64_t d_stride_l, const int32_t* lengths, const int32_t* argmax,
+                    const float* grad_scores, int64_t g_stride_n, int64_t g_stride_b, void* dQ, void* dD,
+                    int64_t Nq, int64_t B, int64_t Lq, int64_t Ld, int64_t d, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+size_t fmx_bwd_batched_workspace_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t Ld, int64_t d);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,138 @@
+"""GPU parity of the training extensions: doc lengths and batched queries.
+
+flash_maxsim_train(Q, D, doc_lengths) and flash_maxsim_train_batched(Q, D,
+doc_lengths) against the oracle (scores, the argmax the forward saves, and
+the backward formula applied to that argmax: oracle.bwd per query, summed over
+queries for dD), and against float64 autograd through the reference's own
+naive MaxSim (maxsim_naive) on the CPU, which fixes what an empty doc
+contributes (no gradient). Tolerances as in test_gpu_parity.py: scores and
+gradients within 1e-2 of the oracle.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import flash_maxsim_amd as fm
+from conftest import sim, to_np32
+from flash_maxsim_amd.flash_maxsim import _launch_fwd, _prep
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+ATOL = 1e-2
+
+
+def saved_argmax(Qn, Dn, lengths, dtype=torch.float16):
+    Q3 = Qn if Qn.ndim == 3 else Qn[None]
+    Nq, Lq, d = Q3.shape
+    B, Ld = Dn.shape[:2]
+    Qk = _prep(torch.from_numpy(Q3).to(dtype).to(DEV), dtype)
+    Dk = _prep(torch.from_numpy(Dn).to(dtype).to(DEV), dtype)
+    lt = None if lengths is None else torch.as_tensor(lengths, dtype=torch.int32, device=DEV)
+    _, am = _launch_fwd(Qk, Dk, lt, Nq, B, Lq, Ld, d, True, True)
+    return am.cpu().numpy().reshape(Nq, B, Lq)
+
+
+def reference_grads(oracle_mod, Qn, Dn, am, g, lengths):
+    """dQ [Nq, Lq, d], dD [B, Ld, d] in float64 from the oracle's backward,
+    with empty docs' upstream gradient set to zero (they give no gradient)."""
+    Q3 = Qn if Qn.ndim == 3 else Qn[None]
+    g2 = np.array(g, dtype=np.float64).reshape(Q3.shape[0], -1)
+    if lengths is not None:
+        g2[:, np.asarray(lengths) <= 0] = 0.0
+    dQ = np.zeros(Q3.shape)
+    dD = np.zeros(Dn.shape)
+    for qi in range(Q3.shape[0]):
+        a, b = oracle_mod.bwd(Q3[qi], Dn, am[qi], g2[qi])
+        dQ[qi] = a
+        dD += b
+    return dQ, dD
+
+
+@pytest.mark.parametrize("B, Lq, Ld, d", [(12, 32, 70, 128), (8, 300, 40, 128), (6, 64, 90, 1024), (9, 16, 33, 96)])
+def test_train_with_doc_lengths(oracle_mod, B, Lq, Ld, d):
+    Q = sim((Lq, d), 1100 + d)
+    D = sim((B, Ld, d), 1101 + Lq)
+    lengths = torch.randint(1, Ld + 1, (B,), generator=torch.Generator().manual_seed(B), dtype=torch.int32)
+    lengths[1] = 0
+    lengths[2] = Ld + 7  # clamps to Ld
+    Qg, Dg = Q.to(DEV).requires_grad_(True), D.to(DEV).requires_grad_(True)
+    s = fm.flash_maxsim_train(Qg, Dg, lengths.to(DEV))
+    g = torch.linspace(-1.0, 2.0, B)
+    (s.masked_fill(torch.isinf(s), 0.0) * g.to(DEV)).sum().backward()
+    Qn, Dn = to_np32(Q), to_np32(D)
+    ref = oracle_mod.maxsim(Qn, Dn, lengths.numpy())[0]
+    got = s.detach().double().cpu().numpy()
+    np.testing.assert_array_equal(np.isinf(got), np.isinf(ref))
+    assert np.abs(got[np.isfinite(ref)] - ref[np.isfinite(ref)]).max() <= ATOL
+    am = saved_argmax(Qn, Dn, lengths.numpy())
+    clamped = np.clip(lengths.numpy(), 0, Ld)
+    for b in range(B):
+        if clamped[b] > 0:
+            assert (am[0, b] < clamped[b]).all()
+    dQ_ref, dD_ref = reference_grads(oracle_mod, Qn, Dn, am, g.numpy(), clamped)
+    np.testing.assert_allclose(Qg.grad.double().cpu().numpy(), dQ_ref[0], rtol=2e-3, atol=ATOL)
+    np.testing.assert_allclose(Dg.grad.double().cpu().numpy(), dD_ref, rtol=2e-3, atol=ATOL)
+    assert not Dg.grad[1].any()  # the empty doc gets no gradient
+
+
+@pytest.mark.parametrize("Nq, B, Lq, Ld, d", [(3, 10, 32, 60, 128), (16, 20, 32, 40, 128), (4, 6, 100, 50, 1024),
+                                              (2, 7, 24, 30, 64)])
+def test_train_batched(oracle_mod, Nq, B, Lq, Ld, d):
+    Q = sim((Nq, Lq, d), 1200 + Nq)
+    D = sim((B, Ld, d), 1201 + d)
+    lengths = torch.randint(0, Ld + 1, (B,), generator=torch.Generator().manual_seed(Nq), dtype=torch.int32)
+    lengths[0] = 0
+    Qg, Dg = Q.to(DEV).requires_grad_(True), D.to(DEV).requires_grad_(True)
+    s = fm.flash_maxsim_train_batched(Qg, Dg, lengths.to(DEV))
+    assert s.shape == (Nq, B)
+    g = torch.randn(Nq, B, generator=torch.Generator().manual_seed(7))
+    (s.masked_fill(torch.isinf(s), 0.0) * g.to(DEV)).sum().backward()
+    Qn, Dn = to_np32(Q), to_np32(D)
+    ref = oracle_mod.maxsim(Qn, Dn, lengths.numpy())
+    got = s.detach().double().cpu().numpy()
+    np.testing.assert_array_equal(np.isinf(got), np.isinf(ref))
+    assert np.abs(got[np.isfinite(ref)] - ref[np.isfinite(ref)]).max() <= ATOL
+    # scores equal the batched forward's
+    np.testing.assert_array_equal(s.detach().cpu().numpy(),
+                                  fm.flash_maxsim_batched(Q.to(DEV), D.to(DEV), lengths.to(DEV)).cpu().numpy())
+    am = saved_argmax(Qn, Dn, lengths.numpy())
+    dQ_ref, dD_ref = reference_grads(oracle_mod, Qn, Dn, am, g.numpy(), lengths.numpy())
+    np.testing.assert_allclose(Qg.grad.double().cpu().numpy(), dQ_ref, rtol=2e-3, atol=ATOL)
+    np.testing.assert_allclose(Dg.grad.double().cpu().numpy(), dD_ref, rtol=2e-3, atol=ATOL)
+
+
+def test_train_lengths_match_naive_autograd():
+    """Float64 autograd through maxsim_naive on the CPU (the reference's own
+    oracle function) fixes the gradients, empty doc included."""
+    Q = sim((20, 64), 1300)
+    D = sim((7, 30, 64), 1301)
+    lengths = torch.tensor([30, 0, 1, 17, 29, 5, 30], dtype=torch.int32)
+    Qd, Dd = Q.double().requires_grad_(True), D.double().requires_grad_(True)
+    ref = fm.maxsim_naive(Qd, Dd, lengths)
+    fin = torch.isfinite(ref)
+    (ref[fin] * torch.arange(1.0, 1.0 + int(fin.sum()), dtype=torch.float64)).sum().backward()
+    Qg, Dg = Q.to(DEV).requires_grad_(True), D.to(DEV).requires_grad_(True)
+    s = fm.flash_maxsim_train(Qg, Dg, lengths.to(DEV))
+    sf = torch.isfinite(s)
+    assert torch.equal(sf.cpu(), fin)
+    (s[sf] * torch.arange(1.0, 1.0 + int(sf.sum()), device=DEV)).sum().backward()
+    np.testing.assert_allclose(Qg.grad.double().cpu().numpy(), Qd.grad.numpy(), rtol=2e-3, atol=ATOL)
+    np.testing.assert_allclose(Dg.grad.double().cpu().numpy(), Dd.grad.numpy(), rtol=2e-3, atol=ATOL)
+
+
+def test_train_batched_deterministic_and_grad_only_q():
+    Q = sim((8, 32, 128), 1400).to(DEV)
+    D = sim((30, 64, 128), 1401).to(DEV)
+    outs = []
+    for _ in range(2):
+        Qg, Dg = Q.clone().requires_grad_(True), D.clone().requires_grad_(True)
+        fm.flash_maxsim_train_batched(Qg, Dg).sum().backward()
+        outs.append((Qg.grad.clone(), Dg.grad.clone()))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    Qg = Q.clone().requires_grad_(True)
+    fm.flash_maxsim_train_batched(Qg, D).sum().backward()
+    assert torch.equal(Qg.grad, outs[0][0])
