@@ -9,15 +9,27 @@
 // maximum), so the k largest keys are exactly the k best (score, index) pairs
 // and all keys are distinct.
 //
-// A workgroup of 1024 threads loads a chunk of C keys into LDS, bitonic-sorts
-// it descending and writes its first k keys. Level 0 reads scores; further
-// levels read the previous level's keys (C / k times fewer each level) until
-// one chunk per row remains, whose workgroup writes values and indices.
+// A workgroup of 1024 threads holds a chunk of up to C = 1024*E keys in
+// registers and finds its k largest by radix selection: passes over 8-bit
+// digits (most significant first) build a 256-bin LDS histogram of the keys
+// still matching the selected prefix, and one wave finds the bin that holds
+// the k-th largest; selection stops as soon as that bin holds exactly the
+// keys still needed. Keys are distinct, so the selected set is exactly the
+// keys whose leading bits are >= the final prefix. A block scan compacts them
+// into LDS. Intermediate levels write the chunk's k keys (unordered); the last
+// level ranks them by counting (rank = keys greater than it) and writes values
+// and indices best first. Rows longer than C run several levels, each C / k
+// times shorter.
 #include "fmx_device.h"
 #include "fmx_kernels.h"
 
 namespace fmx {
 namespace {
+
+// Inverse of ord_of for numbers (NaN maps back to a canonical NaN, -0 to +0).
+__device__ __forceinline__ float float_of(uint32_t o) {
+  return __builtin_bit_cast(float, (o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
 
 __device__ __forceinline__ uint32_t ord_of(float f) {
   uint32_t u = __builtin_bit_cast(uint32_t, f);
@@ -26,92 +38,228 @@ __device__ __forceinline__ uint32_t ord_of(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Descending bitonic sort of C keys in LDS by 1024 threads.
-template <int C>
-__device__ __forceinline__ void bitonic_desc(uint64_t* keys) {
-  for (int size = 2; size <= C; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+constexpr int kTopkThreads = 1024;
+constexpr int kTopkMaxK = 1024;                  // FMX_MAX_TOPK
+constexpr int kTopkC = kTopkThreads * 16;       // keys per chunk (16 per thread)
+
+__device__ __forceinline__ int block_exclusive_scan(int v, int* wave_tot, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int inc = v;
 #pragma unroll
-      for (int p = threadIdx.x; p < C / 2; p += 1024) {
-        const int i = 2 * stride * (p / stride) + (p % stride);
-        const int j = i + stride;
-        const bool desc = (i & size) == 0;  // direction of this bitonic block
-        const uint64_t a = keys[i], b = keys[j];
-        if ((a < b) == desc) {
-          keys[i] = b;
-          keys[j] = a;
-        }
-      }
-      __syncthreads();
-    }
+  for (int s = 1; s < 64; s <<= 1) {
+    const int o = __shfl_up(inc, s);
+    if (lane >= s) inc += o;
   }
+  if (lane == 63) wave_tot[wave] = inc;
+  __syncthreads();
+  if (wave == 0) {
+    int t = lane < kTopkThreads / 64 ? wave_tot[lane] : 0;
+    int ti = t;
+#pragma unroll
+    for (int s = 1; s < 16; s <<= 1) {
+      const int o = __shfl_up(ti, s);
+      if (lane >= s) ti += o;
+    }
+    if (lane < kTopkThreads / 64) wave_tot[lane] = ti - t;  // exclusive wave offsets
+    if (lane == kTopkThreads / 64 - 1) *total = ti;
+  }
+  __syncthreads();
+  return wave_tot[wave] + inc - v;
 }
 
 // grid (chunks, rows). Level 0 (keys_in == null): row r's chunk c covers
-// indices [c*C, c*C + C) of scores[r, :n]. Otherwise keys_in[r, :n].
-// Output: the chunk's top min(k, count) keys to keys_out[r, c*k ...], padded
-// with 0 (a key below every real one) up to k; or, at the last level, values
-// and indices.
-template <int C>
-__global__ void __launch_bounds__(1024) topk_level_kernel(const float* scores, int64_t s_stride, const uint64_t* keys_in,
-                                                          int64_t n, int k, uint64_t* keys_out, float* values,
-                                                          int64_t* indices, int64_t o_stride) {
-  __shared__ uint64_t keys[C];
+// indices [c*C, c*C + C) of scores[r, :n]. Otherwise keys_in[r, :n] (0 = no key).
+// Output: the chunk's k best keys to keys_out[r, c*k ...] (0-padded when the
+// chunk holds fewer), or, at the last level, values and indices, best first.
+template <int kTopkE>  // keys per thread: the chunk is 1024 * kTopkE keys
+__global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* scores, int64_t s_stride,
+                                                                 const uint64_t* keys_in, int64_t n, int k,
+                                                                 uint64_t* keys_out, float* values,
+                                                                 int64_t* indices, int64_t o_stride) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint64_t sel[kTopkMaxK];
+  __shared__ int wave_tot[kTopkThreads / 64];
+  __shared__ uint64_t wmin[kTopkThreads / 64], wmax[kTopkThreads / 64];
+  __shared__ int bcast[4];
   const int64_t row = blockIdx.y;
-  const int64_t c0 = (int64_t)blockIdx.x * C;
-  for (int t = threadIdx.x; t < C; t += 1024) {
-    const int64_t i = c0 + t;
-    uint64_t key = 0;
-    if (i < n) {
-      if (!keys_in) {
-        key = ((uint64_t)ord_of(scores[row * s_stride + i]) << 32) | (uint32_t)~(uint32_t)i;
-      } else {
-        key = keys_in[row * n + i];
+  const int64_t c0 = (int64_t)blockIdx.x * (kTopkThreads * kTopkE);
+  const int tid = threadIdx.x;
+
+  uint64_t key[kTopkE];
+  int valid = 0;
+#pragma unroll
+  for (int e = 0; e < kTopkE; ++e) {
+    const int64_t i = c0 + (int64_t)e * kTopkThreads + tid;
+    uint64_t kv = 0;
+    if (i < n) kv = keys_in ? keys_in[row * n + i]
+                            : (((uint64_t)ord_of(scores[row * s_stride + i]) << 32) | (uint32_t)~(uint32_t)i);
+    key[e] = kv;
+    valid += kv != 0;
+  }
+  // keys present in this chunk (0-keys are padding from an earlier level)
+  int total;
+  {
+    int* tot = &bcast[3];
+    block_exclusive_scan(valid, wave_tot, tot);
+    total = *tot;
+  }
+  const int want = total < k ? total : k;
+
+  // ---- radix selection of the `want` largest keys ----
+  // Digits start at the highest bit where the chunk's keys differ (block min
+  // and max): scores of one query sit in a narrow range, and digits over their
+  // common leading bits would put every key in one histogram bin.
+  uint64_t prefix = 0;
+  int shift = 64, krem = want;
+  if (want > 0 && want < total) {
+    uint64_t mn = ~(uint64_t)0, mx = 0;
+#pragma unroll
+    for (int e = 0; e < kTopkE; ++e) {
+      if (key[e] != 0) {
+        mn = key[e] < mn ? key[e] : mn;
+        mx = key[e] > mx ? key[e] : mx;
       }
     }
-    keys[t] = key;
+#pragma unroll
+    for (int s = 1; s < 64; s <<= 1) {
+      const uint64_t omn = __shfl_xor(mn, s), omx = __shfl_xor(mx, s);
+      mn = omn < mn ? omn : mn;
+      mx = omx > mx ? omx : mx;
+    }
+    if ((tid & 63) == 0) {
+      wmin[tid >> 6] = mn;
+      wmax[tid >> 6] = mx;
+    }
+    __syncthreads();
+    mn = wmin[0];
+    mx = wmax[0];
+    for (int w = 1; w < kTopkThreads / 64; ++w) {
+      mn = wmin[w] < mn ? wmin[w] : mn;
+      mx = wmax[w] > mx ? wmax[w] : mx;
+    }
+    shift = 64 - __builtin_clzll(mn ^ mx);  // keys differ only below bit `shift` (mn != mx)
+    prefix = shift == 64 ? 0 : mx >> shift;
+  } else {
+    krem = 0;  // nothing to choose: all or none of the keys
   }
+  while (krem > 0 && shift > 0) {
+    const int dbits = shift < 8 ? shift : 8;
+    const int nshift = shift - dbits;
+    if (tid < 256) hist[tid] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < kTopkE; ++e) {
+      const uint64_t kv = key[e];
+      if (kv != 0 && (shift == 64 || (kv >> shift) == prefix))
+        atomicAdd(&hist[(uint32_t)(kv >> nshift) & ((1u << dbits) - 1u)], 1u);
+    }
+    __syncthreads();
+    if (tid < 64) {
+      // lane l holds bins 4l .. 4l+3; suffix sums from the top bin down
+      uint32_t h[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) h[j] = hist[4 * tid + j];
+      const uint32_t lane_tot = h[0] + h[1] + h[2] + h[3];
+      uint32_t suf = lane_tot;  // sum over lanes >= tid
+#pragma unroll
+      for (int s = 1; s < 64; s <<= 1) {
+        const uint32_t o = __shfl_down(suf, s);
+        if (tid + s < 64) suf += o;
+      }
+      uint32_t above = suf - lane_tot;  // keys in bins of higher lanes
+#pragma unroll
+      for (int j = 3; j >= 0; --j) {
+        if (above < (uint32_t)krem && (uint32_t)krem <= above + h[j]) {
+          bcast[0] = 4 * tid + j;
+          bcast[1] = krem - (int)above;       // still needed from this bin
+          bcast[2] = (int)h[j];
+        }
+        above += h[j];
+      }
+    }
+    __syncthreads();
+    const int digit = bcast[0], need = bcast[1], inbin = bcast[2];
+    __syncthreads();  // bcast is rewritten by the next pass
+    prefix = (shift == 64 ? 0 : prefix << dbits) | (uint64_t)digit;
+    shift = nshift;
+    krem = need;
+    if (inbin == need) break;  // every key of this bin is selected
+  }
+
+  // ---- compaction: keys whose leading (64 - shift) bits are >= prefix ----
+  // (all keys when want == total, none when want == 0)
+  int mine = 0;
+#pragma unroll
+  for (int e = 0; e < kTopkE; ++e) {
+    const uint64_t kv = key[e];
+    mine += kv != 0 && want > 0 && (shift == 64 ? true : (kv >> shift) >= prefix);
+  }
+  int nsel;
+  int pos = block_exclusive_scan(mine, wave_tot, &bcast[3]);
+  nsel = bcast[3];
+#pragma unroll
+  for (int e = 0; e < kTopkE; ++e) {
+    const uint64_t kv = key[e];
+    if (kv != 0 && want > 0 && (shift == 64 ? true : (kv >> shift) >= prefix)) {
+      if (pos < kTopkMaxK) sel[pos] = kv;
+      ++pos;
+    }
+  }
+  if (nsel > want) nsel = want;  // exactly `want` by construction; never past sel
   __syncthreads();
-  bitonic_desc<C>(keys);
-  if (values) {  // values re-read by index: the input's exact bits (NaN payloads, signed zeros)
-    for (int t = threadIdx.x; t < k; t += 1024) {
-      const int64_t idx = (int64_t)(uint32_t)~(uint32_t)keys[t];
-      values[row * o_stride + t] = scores[row * s_stride + idx];
-      indices[row * o_stride + t] = idx;
+
+  if (values) {
+    for (int t = tid; t < nsel; t += kTopkThreads) {
+      const uint64_t kv = sel[t];
+      int rank = 0;
+      for (int u = 0; u < nsel; ++u) rank += sel[u] > kv;
+      const int64_t idx = (int64_t)(uint32_t)~(uint32_t)kv;
+      if (rank < k) {  // idx comes from a real key: a valid index of the row
+        // The key's value, or, where the key lost the input's bits (zeros, NaN),
+        // the input itself.
+        float v = float_of((uint32_t)(kv >> 32));
+        if (v == 0.f || v != v) v = scores[row * s_stride + idx];
+        values[row * o_stride + rank] = v;
+        indices[row * o_stride + rank] = idx;
+      }
     }
   } else {
     const int64_t nout = (int64_t)gridDim.x * k;
-    for (int t = threadIdx.x; t < k; t += 1024) keys_out[row * nout + (int64_t)blockIdx.x * k + t] = keys[t];
+    for (int t = tid; t < k; t += kTopkThreads)
+      keys_out[row * nout + (int64_t)blockIdx.x * k + t] = t < nsel ? sel[t] : 0;
   }
 }
 
-template <int C>
 hipError_t run_levels(const TopkArgs& a, hipStream_t s) {
   int64_t n = a.B;
   const uint64_t* in = nullptr;
-  uint64_t* bufs[2] = {a.ws, a.ws + topk_ws_keys(a.Nq, a.B, a.k, C) / 2};
+  uint64_t* bufs[2] = {a.ws, a.ws + topk_ws_keys(a.Nq, a.B, a.k, kTopkC) / 2};
   int which = 0;
-  bool first = true;
   while (true) {
-    const int64_t chunks = (n + C - 1) / C;
+    const int64_t chunks = (n + kTopkC - 1) / kTopkC;
     const bool last = chunks == 1;
     if (chunks > 0x7fffffff || a.Nq > 65535) return hipErrorInvalidValue;
     uint64_t* out = last ? nullptr : bufs[which];
-    hipLaunchKernelGGL((topk_level_kernel<C>), dim3((unsigned)chunks, (unsigned)a.Nq), dim3(1024), 0, s, a.scores,
-                       a.s_stride, first ? nullptr : in, n, a.k, out, last ? a.values : nullptr,
-                       last ? a.indices : nullptr, a.o_stride);
+    // a single chunk holds no more keys per thread than the row needs
+    auto kern = n <= 4 * kTopkThreads ? topk_level_kernel<4>
+              : n <= 8 * kTopkThreads ? topk_level_kernel<8> : topk_level_kernel<16>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)chunks, (unsigned)a.Nq), dim3(kTopkThreads), 0, s, a.scores,
+                       a.s_stride, in, n, a.k, out, last ? a.values : nullptr, last ? a.indices : nullptr,
+                       a.o_stride);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || last) return e;
     in = out;
     n = chunks * a.k;
     which ^= 1;
-    first = false;
   }
 }
 
 }  // namespace
 
-int topk_chunk(int k) { return k <= 512 ? 2048 : 4096; }
+int topk_chunk(int k) {
+  (void)k;
+  return kTopkC;
+}
 
 // Keys of both ping-pong buffers: level 1 holds ceil(B / C) * k keys per row,
 // every later level fewer.
@@ -121,8 +269,6 @@ int64_t topk_ws_keys(int64_t Nq, int64_t B, int64_t k, int64_t C) {
   return 2 * Nq * chunks * k;
 }
 
-hipError_t launch_topk(const TopkArgs& a, hipStream_t s) {
-  return topk_chunk(a.k) == 2048 ? run_levels<2048>(a, s) : run_levels<4096>(a, s);
-}
+hipError_t launch_topk(const TopkArgs& a, hipStream_t s) { return run_levels(a, s); }
 
 }  // namespace fmx
