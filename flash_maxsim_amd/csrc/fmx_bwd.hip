@@ -58,16 +58,19 @@ __device__ __forceinline__ void load8(const uint16_t* row, int k0, int d, float 
 }
 
 // Stores elements k0 .. k0+7 (those < d); 16-byte stores need d % 8 == 0 so
-// that every row of the contiguous output starts 16-byte aligned.
+// that every row of the contiguous output starts 16-byte aligned. dD is
+// written once and read only by the optimiser later: non-temporal stores
+// stream it out instead of leaving it dirty in the caches, where its
+// write-back would compete with the next forward's reads.
 template <bool BF>
 __device__ __forceinline__ void store8(uint16_t* row, int k0, int d, const float (&x)[8]) {
   if ((d & 7) == 0) {
-    uint4 v;
-    v.x = (uint32_t)Elem<BF>::from_f(x[0]) | ((uint32_t)Elem<BF>::from_f(x[1]) << 16);
-    v.y = (uint32_t)Elem<BF>::from_f(x[2]) | ((uint32_t)Elem<BF>::from_f(x[3]) << 16);
-    v.z = (uint32_t)Elem<BF>::from_f(x[4]) | ((uint32_t)Elem<BF>::from_f(x[5]) << 16);
-    v.w = (uint32_t)Elem<BF>::from_f(x[6]) | ((uint32_t)Elem<BF>::from_f(x[7]) << 16);
-    *reinterpret_cast<uint4*>(row + k0) = v;
+    u32x4_t v;
+    v[0] = (uint32_t)Elem<BF>::from_f(x[0]) | ((uint32_t)Elem<BF>::from_f(x[1]) << 16);
+    v[1] = (uint32_t)Elem<BF>::from_f(x[2]) | ((uint32_t)Elem<BF>::from_f(x[3]) << 16);
+    v[2] = (uint32_t)Elem<BF>::from_f(x[4]) | ((uint32_t)Elem<BF>::from_f(x[5]) << 16);
+    v[3] = (uint32_t)Elem<BF>::from_f(x[6]) | ((uint32_t)Elem<BF>::from_f(x[7]) << 16);
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(row + k0));
   } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e)
@@ -87,16 +90,16 @@ __device__ __forceinline__ int doc_len(const BwdArgs& a, int b) {
 // chunk), one grid row per chunk of docs; ws[chunk][r][k] = sum over the
 // chunk's docs, in order.
 template <bool BF>
-__global__ void __launch_bounds__(256) bwd_dq_partial_kernel(BwdArgs a) {
+__device__ __forceinline__ void dq_partial_block(const BwdArgs& a, int bx, int by) {
   const int nkc = (a.d + 7) >> 3;
   const int64_t rows = (int64_t)a.Nq * a.Lq;
-  const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t tid = (int64_t)bx * 256 + threadIdx.x;
   if (tid >= rows * nkc) return;
   const int64_t r = tid / nkc;
   const int k0 = (int)(tid - r * nkc) * 8;
   const int qi = (int)(r / a.Lq), q = (int)(r - (int64_t)qi * a.Lq);
   const int per = (a.B + a.nchunk - 1) / a.nchunk;
-  const int b0 = blockIdx.y * per;
+  const int b0 = by * per;
   const int b1 = min(a.B, b0 + per);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   const uint16_t* D = static_cast<const uint16_t*>(a.D);
@@ -112,7 +115,7 @@ __global__ void __launch_bounds__(256) bwd_dq_partial_kernel(BwdArgs a) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] = fmaf(gb, x[e], acc[e]);
   }
-  float* out = a.ws + ((int64_t)blockIdx.y * rows + r) * a.d + k0;
+  float* out = a.ws + ((int64_t)by * rows + r) * a.d + k0;
 #pragma unroll
   for (int e = 0; e < 8; ++e)
     if (k0 + e < a.d) out[e] = acc[e];
@@ -125,7 +128,8 @@ __global__ void __launch_bounds__(256) bwd_dq_finalize_kernel(BwdArgs a) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
   float s = 0.f;
-  for (int c = 0; c < a.nchunk; ++c) s += a.ws[(int64_t)c * n + i];
+#pragma unroll 8
+  for (int c = 0; c < a.nchunk; ++c) s += a.ws[(int64_t)c * n + i];  // chunk order: deterministic
   static_cast<uint16_t*>(a.dQ)[i] = Elem<BF>::from_f(s);
 }
 
@@ -135,11 +139,9 @@ constexpr int kEntryBits = 13;  // (query, token) entries per doc < 2^13
 // row << 13 | entry, sorted ascending (bitonic), and a bitmap of picked rows.
 // A picked row's entries are then contiguous and in entry order.
 template <bool BF>
-__global__ void __launch_bounds__(256) bwd_dd_kernel(BwdArgs a) {
-  extern __shared__ uint32_t smem[];
+__device__ __forceinline__ void dd_block(const BwdArgs& a, int b, uint32_t* smem) {
   uint32_t* keys = smem;
   uint32_t* hit = smem + a.sort_n;
-  const int b = blockIdx.x;
   const int nkc = (a.d + 7) >> 3;
   const int NL = a.Nq * a.Lq;
   const bool empty = a.lengths && doc_len(a, b) == 0;
@@ -203,6 +205,19 @@ __global__ void __launch_bounds__(256) bwd_dd_kernel(BwdArgs a) {
   }
 }
 
+template <bool BF>
+__global__ void __launch_bounds__(256) bwd_dq_partial_kernel(BwdArgs a) {
+  dq_partial_block<BF>(a, blockIdx.x, blockIdx.y);
+}
+
+template <bool BF>
+__global__ void __launch_bounds__(256) bwd_dd_kernel(BwdArgs a) {
+  extern __shared__ uint32_t smem[];
+  dd_block<BF>(a, blockIdx.x, smem);
+}
+
+// dQ and dD run as separate launches: interleaving the read-bound dQ blocks
+// with the write-bound dD blocks in one grid measured 15 % slower on config 5.
 template <bool BF>
 hipError_t launch_bwd_t(const BwdArgs& a, hipStream_t s) {
   const int nkc = (a.d + 7) >> 3;

@@ -14,6 +14,9 @@
 // query block nb in wave order (deterministic), applies the uint8 affine
 // epilogue and the length mask, and folds the rows into its running max. The
 // max therefore always sees the full-d similarity, never a partial one.
+// The partial buffer is double-buffered by tile parity, so one barrier per
+// tile suffices: tile t+2 rewrites tile t's buffer only after every wave has
+// passed tile t+1's barrier, i.e. after it finished reducing tile t.
 #include "fmx_kernels.h"
 #include "fmx_tile.h"
 
@@ -31,7 +34,7 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
   constexpr bool BF = KindInfo<KIND>::bf;
   constexpr bool U8 = KIND == KIND_U8;
   static_assert(NQB <= NW, "one owning wave per query block");
-  __shared__ f32x4_t part[NW][NQB][64];
+  __shared__ f32x4_t part[2][NW][NQB][64];
   __shared__ float qs_part[U8 ? NW : 1][QROWS];
   __shared__ float red_m[QROWS];
   __shared__ int red_i[ARGMAX ? QROWS : 1];
@@ -134,13 +137,13 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
           f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int t = 0; t < KSW; ++t) acc = mfma16x16x32<BF>(af[t], qf[nb][t], acc);
-          part[wave][nb][lane] = acc;
+          part[tile & 1][wave][nb][lane] = acc;
         }
         __syncthreads();
         if (owner) {
-          f32x4_t S = part[0][wave][lane];
+          f32x4_t S = part[tile & 1][0][wave][lane];
 #pragma unroll
-          for (int w = 1; w < NW; ++w) S += part[w][wave][lane];
+          for (int w = 1; w < NW; ++w) S += part[tile & 1][w][wave][lane];
           if constexpr (U8) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) S[r] = fmaf(sc[r], S[r], off[r] * qsum);
@@ -163,7 +166,6 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
             m = vmax(m, vmax(vmax(S[0], S[1]), vmax(S[2], S[3])));
           }
         }
-        __syncthreads();
       }
     }
   }
