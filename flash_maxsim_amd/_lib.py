@@ -47,7 +47,7 @@ _SIGNATURES = {
     "fmx_fwd_sparse_workspace_bytes": (_size, [_i64, _i64, _i64, _i64]),
     "fmx_quantize_int8": (
         _int,
-        [_int, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr, _i64, _ptr, _ptr, _i64, _ptr],
+        [_int, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _i64, _ptr],
     ),
     "fmx_fwd_packed": (
         _int,

@@ -306,7 +306,7 @@ int fmx_fwd_int8_packed(const void* Q, int64_t q_stride_l, int64_t Lq, const uin
 }
 
 int fmx_quantize_int8(int src_dtype, const void* src, int64_t s_stride_b, int64_t s_stride_l, int64_t B, int64_t Ld,
-                      int64_t d, const int32_t* lengths, const int64_t* tok_group, uint8_t* codes,
+                      int64_t d, const int32_t* lengths, const int64_t* tok_group, int64_t tok_rows, uint8_t* codes,
                       int64_t c_stride_l, void* scales, void* mins, int64_t sm_stride_b, void* stream) {
   int esz;
   switch (src_dtype) {
@@ -320,6 +320,7 @@ int fmx_quantize_int8(int src_dtype, const void* src, int64_t s_stride_b, int64_
   if (s_stride_l < d || c_stride_l < d || s_stride_b < 0)
     return fail(FMX_ERR_INVALID, "row strides must be >= d");
   if (!tok_group && (sm_stride_b < Ld)) return fail(FMX_ERR_INVALID, "scale doc stride < Ld");
+  if (tok_group && tok_rows < 0) return fail(FMX_ERR_INVALID, "tok_rows=%lld must be >= 0", (long long)tok_rows);
   if (B == 0 || Ld == 0) return ok();
   if (!src || !codes || !scales || !mins) return fail(FMX_ERR_INVALID, "src, codes, scales and mins must be non-null");
   if ((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(mins)) & 1u)
@@ -335,6 +336,7 @@ int fmx_quantize_int8(int src_dtype, const void* src, int64_t s_stride_b, int64_
   a.esz = esz;
   a.lengths = lengths;
   a.tok_group = tok_group;
+  a.tok_rows = tok_rows;
   a.codes = codes;
   a.c_stride_l = c_stride_l;
   a.scales = scales;

@@ -93,6 +93,7 @@ struct QuantArgs {
   int esz;                    // bytes per source element
   const int32_t* lengths;     // [B] valid tokens per doc (packed output), or null (= Ld)
   const int64_t* tok_group;   // packed output: doc b starts at row 4*tok_group[b]; null = padded
+  int64_t tok_rows;           // packed output: rows of codes/scales/mins (rows outside are skipped)
   uint8_t* codes;             // padded [B, Ld, d] (row b*Ld + j) or packed [T, d]; row stride c_stride_l
   int64_t c_stride_l;
   void* scales;               // fp16 bits: padded [B, Ld] (doc stride sm_stride_b) or packed [T]

@@ -151,8 +151,9 @@ __global__ void __launch_bounds__(256) quantize_kernel(QuantArgs a) {
 #pragma unroll
     for (int k = 0; k < R; ++k) {
       const int64_t j = jbase + k;
-      const int mode = j >= jend ? 0 : (j >= len ? 1 : 2);  // none / packed zero row / quantise
       const int64_t orow = obase + j;
+      int mode = j >= jend ? 0 : (j >= len ? 1 : 2);  // none / packed zero row / quantise
+      if (packed && (orow < 0 || orow >= a.tok_rows)) mode = 0;  // outside the output: skipped
       uint8_t* crow = a.codes + orow * a.c_stride_l;
       const int64_t smi = packed ? orow : b * a.sm_stride_b + j;
       uint16_t* sp = static_cast<uint16_t*>(a.scales) + smi;

@@ -94,7 +94,7 @@ def quantize_int8_packed(D: torch.Tensor, doc_lengths=None) -> PackedInt8Docs:
         with _device_guard(dev):
             rc = lib.fmx_quantize_int8(
                 _SRC_CODES[src.dtype], src.data_ptr(), src.stride(0), src.stride(1), B, Ld, d, lengths.data_ptr(),
-                tok_group.data_ptr(), codes.data_ptr(), d, scales.data_ptr(), mins.data_ptr(), 0,
+                tok_group.data_ptr(), T, codes.data_ptr(), d, scales.data_ptr(), mins.data_ptr(), 0,
                 _lib.stream_of(src),
             )
         _lib.check(rc)

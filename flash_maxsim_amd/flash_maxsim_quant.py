@@ -68,7 +68,7 @@ def _quantize_gpu(D: torch.Tensor):
     lib = _lib.load()
     with _device_guard(dev):
         rc = lib.fmx_quantize_int8(
-            _SRC_CODES[src.dtype], src.data_ptr(), src.stride(0), src.stride(1), B, Ld, d, None, None,
+            _SRC_CODES[src.dtype], src.data_ptr(), src.stride(0), src.stride(1), B, Ld, d, None, None, 0,
             codes.data_ptr(), d, scales.data_ptr(), mins.data_ptr(), Ld, _lib.stream_of(src),
         )
     _lib.check(rc)

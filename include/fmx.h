@@ -136,13 +136,13 @@ size_t fmx_fwd_sparse_workspace_bytes(int64_t B, int64_t K, int64_t Ld, int64_t 
  *   scales   [T]         fp16; mins likewise (sm_stride_b unused)
  * and rows len_b .. 4*ceil(len_b/4)-1 of the doc's group are zeroed. The caller
  * lays groups out without overlap (e.g. tok_group = exclusive prefix sum of
- * ceil(len_b / 4)); T >= 4 * (tok_group[B-1] + ceil(len_{B-1} / 4)).
+ * ceil(len_b / 4)) and passes T = tok_rows; rows outside [0, T) are not written.
  *
  * Replaces flash_maxsim/flash_maxsim_quant.py:11-28 (quantize_int8, torch ops
  * there); the packed layout is an extension (no counterpart in the reference).
  */
 int fmx_quantize_int8(int src_dtype, const void* src, int64_t s_stride_b, int64_t s_stride_l, int64_t B, int64_t Ld,
-                      int64_t d, const int32_t* lengths, const int64_t* tok_group, uint8_t* codes,
+                      int64_t d, const int32_t* lengths, const int64_t* tok_group, int64_t tok_rows, uint8_t* codes,
                       int64_t c_stride_l, void* scales, void* mins, int64_t sm_stride_b, void* stream);
 
 /*

@@ -120,14 +120,16 @@ def test_sparse_rejects_bad_arguments(lib):
 
 
 def test_quantize_and_packed_reject_bad_arguments(lib):
-    rc = lib.fmx_quantize_int8(7, FAKE, 300 * 128, 128, 10, 300, 128, None, None, FAKE, 128, FAKE, FAKE, 300, None)
+    rc = lib.fmx_quantize_int8(7, FAKE, 300 * 128, 128, 10, 300, 128, None, None, 0, FAKE, 128, FAKE, FAKE, 300, None)
     assert rc == FMX_ERR_INVALID and "source dtype" in lib.fmx_last_error().decode()
-    rc = lib.fmx_quantize_int8(2, FAKE, 300 * 128, 100, 10, 300, 128, None, None, FAKE, 128, FAKE, FAKE, 300, None)
+    rc = lib.fmx_quantize_int8(2, FAKE, 300 * 128, 100, 10, 300, 128, None, None, 0, FAKE, 128, FAKE, FAKE, 300, None)
     assert rc == FMX_ERR_INVALID and "row strides" in lib.fmx_last_error().decode()
-    rc = lib.fmx_quantize_int8(2, FAKE, 300 * 128, 128, 10, 300, 128, None, None, FAKE, 128, FAKE + 1, FAKE, 300,
+    rc = lib.fmx_quantize_int8(2, FAKE, 300 * 128, 128, 10, 300, 128, None, None, 0, FAKE, 128, FAKE + 1, FAKE, 300,
                                None)
     assert rc == FMX_ERR_INVALID and "2-byte aligned" in lib.fmx_last_error().decode()
-    assert lib.fmx_quantize_int8(2, None, 0, 128, 0, 300, 128, None, None, None, 128, None, None, 300, None) == FMX_OK
+    rc = lib.fmx_quantize_int8(2, FAKE, 300 * 128, 128, 10, 300, 128, FAKE, FAKE, -1, FAKE, 128, FAKE, FAKE, 0, None)
+    assert rc == FMX_ERR_INVALID and "tok_rows" in lib.fmx_last_error().decode()
+    assert lib.fmx_quantize_int8(2, None, 0, 128, 0, 300, 128, None, None, 0, None, 128, None, None, 300, None) == FMX_OK
     rc = lib.fmx_fwd_packed(0, FAKE, 128, 32, FAKE, 128, 1000, None, FAKE, FAKE, 10, 300, 128, None, 0, None)
     assert rc == FMX_ERR_INVALID and "tok_group" in lib.fmx_last_error().decode()
     rc = lib.fmx_fwd_int8_packed(FAKE, 128, 32, FAKE, 128, FAKE, FAKE, 1000, FAKE, None, FAKE, 10, 300, 128,

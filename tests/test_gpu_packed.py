@@ -141,3 +141,31 @@ def test_packed_empty_and_all_empty(oracle_mod):
     x = sim((3, 16, 128), 82, torch.float32)
     pk = fm.quantize_int8_packed(x.to(DEV), torch.zeros(3, dtype=torch.int32))
     assert torch.isneginf(fm.flash_maxsim_int8_packed(Q.to(DEV), pk)).all()
+
+
+def test_quantize_packed_respects_tok_rows(oracle_mod):
+    """Rows at or past tok_rows are never written: the buffer has room past T
+    filled with a sentinel, which must survive."""
+    from flash_maxsim_amd import _lib
+
+    B, Ld, d = 4, 20, 128
+    x = sim((B, Ld, d), 90, torch.float32).to(DEV)
+    lengths = torch.full((B,), Ld, dtype=torch.int32, device=DEV)
+    tg = torch.tensor([0, 5, 10, 15], dtype=torch.int64, device=DEV)  # 80 rows of output
+    T = 50
+    codes = torch.full((80, d), 7, dtype=torch.uint8, device=DEV)
+    scales = torch.full((80,), 7.0, dtype=torch.float16, device=DEV)
+    mins = torch.full((80,), 7.0, dtype=torch.float16, device=DEV)
+    lib = _lib.load()
+    rc = lib.fmx_quantize_int8(_lib.FMX_DTYPE_F32, x.data_ptr(), x.stride(0), x.stride(1), B, Ld, d,
+                               lengths.data_ptr(), tg.data_ptr(), T, codes.data_ptr(), d, scales.data_ptr(),
+                               mins.data_ptr(), 0, _lib.stream_of(x))
+    _lib.check(rc)
+    torch.cuda.synchronize()
+    assert (codes[T:] == 7).all() and (scales[T:] == 7).all() and (mins[T:] == 7).all()
+    c_ref = oracle_mod.quantize_int8(to_np32(x))[0]
+    got = codes.cpu().numpy()
+    for b in range(B):
+        r0 = 4 * int(tg[b])
+        n = max(0, min(Ld, T - r0))
+        np.testing.assert_array_equal(got[r0:r0 + n], c_ref[b, :n])
