@@ -92,6 +92,15 @@ __device__ __forceinline__ f32x16_t mfma32x32x16(u32x4_t a, u32x4_t b, f32x16_t 
 // no canonicalisation of MFMA results in front of it.
 __device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
+// Running max over the four result rows of one MFMA fragment, as a chain of
+// two v_maximum3_f32 (m, r0, r1) and (m, r2, r3). IEEE maximum is commutative
+// and associative (NaN propagates, -0 < +0), so the result does not depend on
+// the fold order; the chain form issues one VALU op fewer than a tree.
+__device__ __forceinline__ float fold_max4(float m, float r0, float r1, float r2, float r3) {
+  m = vmax(vmax(m, r0), r1);
+  return vmax(vmax(m, r2), r3);
+}
+
 // Eight uint8 codes -> eight fp16 values 1024 + code, exactly: v_perm places
 // code byte c under exponent byte 0x64, which is the fp16 value 1024 + c
 // (1024 + c < 2048 fits the 11-bit significand). The uint8 kernels multiply
@@ -129,7 +138,11 @@ __device__ __forceinline__ float query_row_sum(const u32x4_t (&qf)[KS]) {
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int t = 0; t < KS; ++t) acc = mfma16x16x32<false>(ones, qf[t], acc);
-  return acc[0];
+  // The four result rows hold the same sum, so their max is that sum exactly.
+  // Reading all four right away keeps none of the MFMA's result registers
+  // dead: a dead one can be reassigned by the compiler across a branch while
+  // the MFMA is still to write it.
+  return fold_max4(acc[0], acc[1], acc[2], acc[3], acc[0]);
 }
 
 // Mask keeping the first n (0..8) 16-bit elements of an 8-element fragment.

@@ -163,7 +163,7 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
               }
             }
           } else {
-            m = vmax(m, vmax(vmax(S[0], S[1]), vmax(S[2], S[3])));
+            m = fold_max4(m, S[0], S[1], S[2], S[3]);
           }
         }
       }

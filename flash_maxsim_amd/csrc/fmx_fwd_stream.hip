@@ -144,32 +144,45 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
         // branching costs more: those loads still queue behind the real ones.)
         if (i + P < my_n) load_tile<KIND, KS, VEC>(buf[s], dr, wave + NW * (i + P), c, g, koff);
         const int row0 = tile * 16 + 4 * g;
-        const bool tail = tile * 16 + 16 > len;
+        // S of this tile against every query block, folded into the running
+        // maxima. TAIL (the doc's last, partial tile) masks rows past len.
+        // The two instances are chosen by a branch before the MFMAs, so each
+        // keeps its MFMAs and the first VALU reads of their results in one
+        // basic block: the compiler inserts the MFMA-to-VALU wait states within
+        // a block, and a branch between the two (a conditional mask after the
+        // MFMAs) let it place the reads too early.
+        auto score_tile = [&](auto tail_tag) {
+          constexpr bool TAIL = decltype(tail_tag)::value;
 #pragma unroll
-        for (int nb = 0; nb < NQB; ++nb) {
-          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+          for (int nb = 0; nb < NQB; ++nb) {
+            f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int t = 0; t < KS; ++t) acc = mfma16x16x32<BF>(af[t], qf[nb][t], acc);
-          if constexpr (U8) {
+            for (int t = 0; t < KS; ++t) acc = mfma16x16x32<BF>(af[t], qf[nb][t], acc);
+            if constexpr (U8) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] = fmaf(sc[r], acc[r], off[r] * qsum[nb]);
-          }
-          if (tail) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              if (row0 + r >= len) acc[r] = -INFINITY;
-          }
-          if constexpr (ARGMAX) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              if (acc[r] > m[nb]) {
-                m[nb] = acc[r];
-                mi[nb] = row0 + r;
-              }
+              for (int r = 0; r < 4; ++r) acc[r] = fmaf(sc[r], acc[r], off[r] * qsum[nb]);
             }
-          } else {
-            m[nb] = vmax(m[nb], vmax(vmax(acc[0], acc[1]), vmax(acc[2], acc[3])));
+            if constexpr (TAIL) {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) acc[r] = row0 + r < len ? acc[r] : -INFINITY;
+            }
+            if constexpr (ARGMAX) {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                if (acc[r] > m[nb]) {
+                  m[nb] = acc[r];
+                  mi[nb] = row0 + r;
+                }
+              }
+            } else {
+              m[nb] = fold_max4(m[nb], acc[0], acc[1], acc[2], acc[3]);
+            }
           }
+        };
+        if (tile * 16 + 16 > len) {
+          score_tile(std::true_type{});
+        } else {
+          score_tile(std::false_type{});
         }
       }
     }

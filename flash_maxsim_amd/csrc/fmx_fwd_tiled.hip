@@ -79,7 +79,7 @@ __device__ __forceinline__ void fold_rows(f32x4_t acc, int rowj, int len, bool t
       }
     }
   } else {
-    m = vmax(m, vmax(vmax(acc[0], acc[1]), vmax(acc[2], acc[3])));
+    m = fold_max4(m, acc[0], acc[1], acc[2], acc[3]);
   }
 }
 
