@@ -175,33 +175,39 @@ __device__ __forceinline__ void dd_block(const BwdArgs& a, int b, uint32_t* smem
     }
   }
 
+  // Rows are dealt to the four waves; a wave's lanes cover a row's 8-wide
+  // k chunks, so each store instruction writes 64 contiguous chunks and all
+  // row/chunk arithmetic is 32-bit without divisions.
   uint16_t* out = static_cast<uint16_t*>(a.dD) + (int64_t)b * a.Ld * a.d;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  const int64_t zn = (int64_t)a.Ld * nkc;
-  for (int64_t e = threadIdx.x; e < zn; e += 256) {
-    const int row = (int)(e / nkc);
-    const int k0 = (int)(e - (int64_t)row * nkc) * 8;
-    if (!((hit[row >> 5] >> (row & 31)) & 1u)) store8<BF>(out + (int64_t)row * a.d, k0, a.d, zero);
+  for (int row = wave; row < a.Ld; row += 4) {
+    if ((hit[row >> 5] >> (row & 31)) & 1u) continue;  // uniform over the wave
+    uint16_t* orow = out + (int64_t)row * a.d;
+    for (int kc = lane; kc < nkc; kc += 64) store8<BF>(orow, kc * 8, a.d, zero);
   }
   if (empty) return;
   const uint16_t* Q = static_cast<const uint16_t*>(a.Q);
-  const int64_t hn = (int64_t)NL * nkc;
-  for (int64_t w = threadIdx.x; w < hn; w += 256) {
-    const int p = (int)(w / nkc);
-    const int k0 = (int)(w - (int64_t)p * nkc) * 8;
+  for (int p = wave; p < NL; p += 4) {
     const uint32_t j = keys[p] >> kEntryBits;
     if (p > 0 && (keys[p - 1] >> kEntryBits) == j) continue;  // not the first entry of its row
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int p2 = p; p2 < NL && (keys[p2] >> kEntryBits) == j; ++p2) {
-      const int e = (int)(keys[p2] & ((1u << kEntryBits) - 1));
-      const int qi = e / a.Lq, q = e - qi * a.Lq;
-      const float g = a.grad[(int64_t)qi * a.g_n + (int64_t)b * a.g_b];
-      float x[8];
-      load8<BF>(Q + (int64_t)qi * a.sq_n + (int64_t)q * a.sq_l, k0, a.d, x);
+    // The row's entries keys[p .. p2) in entry order, their query rows
+    // weighted by the upstream gradient of (query, doc).
+    for (int kc = lane; kc < nkc; kc += 64) {
+      const int k0 = kc * 8;
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int p2 = p; p2 < NL && (keys[p2] >> kEntryBits) == j; ++p2) {
+        const int e = (int)(keys[p2] & ((1u << kEntryBits) - 1));
+        const int qi = e / a.Lq, q = e - qi * a.Lq;
+        const float g = a.grad[(int64_t)qi * a.g_n + (int64_t)b * a.g_b];
+        float x[8];
+        load8<BF>(Q + (int64_t)qi * a.sq_n + (int64_t)q * a.sq_l, k0, a.d, x);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) acc[k] = fmaf(g, x[k], acc[k]);
+        for (int k = 0; k < 8; ++k) acc[k] = fmaf(g, x[k], acc[k]);
+      }
+      store8<BF>(out + (int64_t)j * a.d, k0, a.d, acc);
     }
-    store8<BF>(out + (int64_t)j * a.d, k0, a.d, acc);
   }
 }
 

@@ -29,7 +29,9 @@ constexpr int kSplitWaves = 8;
 template <int KIND, int NQB, int KSW, bool KMASK, bool ARGMAX, bool VEC>
 __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
   constexpr int NW = kSplitWaves, QROWS = NQB * 16;
-  constexpr int P = KSW >= 8 ? 2 : 3;  // tiles in flight per wave
+  // Tiles in flight per wave: 2 when the query slice takes 128 VGPRs, which
+  // leaves room for the pipelined tile's results next to the buffers.
+  constexpr int P = (KSW >= 8 || NQB * KSW >= 32) ? 2 : 3;
   constexpr int ESZ = KindInfo<KIND>::esz;
   constexpr bool BF = KindInfo<KIND>::bf;
   constexpr bool U8 = KIND == KIND_U8;
@@ -109,7 +111,42 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
 
   float m = -INFINITY;
   int mi = 0;
+  // Owner waves: folds tile rt (its eight partials in part[rt & 1]) into the
+  // running max, with the uint8 affine constants of that tile.
+  auto reduce_tile = [&](int rt, const float (&rsc)[4], const float (&roff)[4]) {
+    if (!owner) return;
+    f32x4_t S = part[rt & 1][0][wave][lane];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) S += part[rt & 1][w][wave][lane];
+    if constexpr (U8) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) S[r] = fmaf(rsc[r], S[r], roff[r] * qsum);
+    }
+    const int row0 = rt * 16 + 4 * g;
+    if (rt * 16 + 16 > len) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (row0 + r >= len) S[r] = -INFINITY;
+    }
+    if constexpr (ARGMAX) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (S[r] > m) {
+          m = S[r];
+          mi = row0 + r;
+        }
+      }
+    } else {
+      m = fold_max4(m, S[0], S[1], S[2], S[3]);
+    }
+  };
+
+  // Software pipeline, one barrier per tile: a wave issues tile t's MFMAs,
+  // then reduces tile t-1 (written before the previous barrier) while they
+  // run, then stores tile t's partials. part[t & 1] is rewritten at tile t+2,
+  // after every owner passed tile t+1's barrier, i.e. finished reducing t.
   Tile<KIND, KSW> buf[P];
+  float psc[4] = {0.f, 0.f, 0.f, 0.f}, poff[4] = {0.f, 0.f, 0.f, 0.f};  // tile t-1 (uint8 docs)
 #pragma unroll
   for (int s = 0; s < P; ++s)
     if (s < ntiles) load_tile<KIND, KSW, VEC>(buf[s], dr, s, c, g, koff);
@@ -131,44 +168,36 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) tile_affine(buf[s].s, buf[s].m, r, sc[r], off[r]);
         }
-        if (tile + P < ntiles) load_tile<KIND, KSW, VEC>(buf[s], dr, tile + P, c, g, koff);
+        f32x4_t acc[NQB];
 #pragma unroll
         for (int nb = 0; nb < NQB; ++nb) {
-          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+          acc[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int t = 0; t < KSW; ++t) acc = mfma16x16x32<BF>(af[t], qf[nb][t], acc);
-          part[tile & 1][wave][nb][lane] = acc;
+          for (int t = 0; t < KSW; ++t) acc[nb] = mfma16x16x32<BF>(af[t], qf[nb][t], acc[nb]);
+        }
+        // Refill slot s after the MFMAs have taken its operands, so the
+        // operands need no copy of their own.
+        if (tile + P < ntiles) load_tile<KIND, KSW, VEC>(buf[s], dr, tile + P, c, g, koff);
+        // The first half of the query blocks finished first: store them, then
+        // reduce the previous tile while the second half runs.
+        constexpr int H = NQB / 2;
+#pragma unroll
+        for (int nb = 0; nb < H; ++nb) part[tile & 1][wave][nb][lane] = acc[nb];
+        if (tile > 0) reduce_tile(tile - 1, psc, poff);
+#pragma unroll
+        for (int nb = H; nb < NQB; ++nb) part[tile & 1][wave][nb][lane] = acc[nb];
+        if constexpr (U8) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            psc[r] = sc[r];
+            poff[r] = off[r];
+          }
         }
         __syncthreads();
-        if (owner) {
-          f32x4_t S = part[tile & 1][0][wave][lane];
-#pragma unroll
-          for (int w = 1; w < NW; ++w) S += part[tile & 1][w][wave][lane];
-          if constexpr (U8) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) S[r] = fmaf(sc[r], S[r], off[r] * qsum);
-          }
-          const int row0 = tile * 16 + 4 * g;
-          if (tile * 16 + 16 > len) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              if (row0 + r >= len) S[r] = -INFINITY;
-          }
-          if constexpr (ARGMAX) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              if (S[r] > m) {
-                m = S[r];
-                mi = row0 + r;
-              }
-            }
-          } else {
-            m = fold_max4(m, S[0], S[1], S[2], S[3]);
-          }
-        }
       }
     }
   }
+  if (ntiles > 0) reduce_tile(ntiles - 1, psc, poff);
 
   // ---- per query token: merge row groups, then sum the pass ----
   if (owner) {
