@@ -435,11 +435,19 @@ int fmx_fwd_sparse(int dtype, const void* Q, int64_t q_stride_l, int64_t Lq, con
   return hip_status(e, "fmx_fwd_sparse launch");
 }
 
-size_t fmx_bwd_batched_workspace_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t Ld, int64_t d) {
-  (void)Ld;
-  if (Nq < 1 || B < 0 || Lq < 1 || d < 1 || Nq * Lq > INT32_MAX) return 0;
+// Backward workspace: the dD index (when dD is written) at offset 0, then the
+// dQ partial sums (when dQ is written).
+static size_t bwd_dd_ws(int64_t Nq, int64_t B, int64_t Lq, int64_t Ld) {
+  return fmx::bwd_dd_index_bytes(B, Nq * Lq, Ld);
+}
+static size_t bwd_dq_ws(int64_t Nq, int64_t B, int64_t Lq, int64_t d) {
   const int64_t rows = Nq * Lq;
   return (size_t)fmx::bwd_dq_chunks((int)B, (int)rows, (int)d) * (size_t)rows * (size_t)d * sizeof(float);
+}
+
+size_t fmx_bwd_batched_workspace_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t Ld, int64_t d) {
+  if (Nq < 1 || B < 0 || Lq < 1 || Ld < 0 || d < 1 || Nq * Lq > INT32_MAX) return 0;
+  return bwd_dd_ws(Nq, B, Lq, Ld) + bwd_dq_ws(Nq, B, Lq, d);
 }
 
 size_t fmx_bwd_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld, int64_t d) {
@@ -465,12 +473,10 @@ int fmx_bwd_batched(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stri
     if (Nq * Lq >= 8192 || Ld >= (1 << 19))
       return fail(FMX_ERR_UNSUPPORTED, "dD kernel covers Nq*Lq < 8192 and Ld < 2^19 (Nq*Lq=%lld, Ld=%lld)",
                   (long long)(Nq * Lq), (long long)Ld);
-    if (fmx::bwd_dd_lds_bytes(Nq * Lq, Ld) > 64 * 1024)
-      return fail(FMX_ERR_UNSUPPORTED, "Nq*Lq=%lld, Ld=%lld exceed the dD kernel's LDS", (long long)(Nq * Lq),
-                  (long long)Ld);
   }
-  const size_t need = fmx_bwd_batched_workspace_bytes(Nq, B, Lq, Ld, d);
-  if (dQ && (!workspace || workspace_bytes < need))
+  const size_t dd_ws = dD ? bwd_dd_ws(Nq, B, Lq, Ld) : 0;
+  const size_t need = dd_ws + (dQ ? bwd_dq_ws(Nq, B, Lq, d) : 0);
+  if (need > 0 && (!workspace || workspace_bytes < need))
     return fail(FMX_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
 
   fmx::BwdArgs a = {};
@@ -481,7 +487,13 @@ int fmx_bwd_batched(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stri
   a.grad = grad_scores;
   a.dQ = dQ;
   a.dD = dD;
-  a.ws = static_cast<float*>(workspace);
+  if (workspace) {
+    char* w = static_cast<char*>(workspace);
+    a.dd_rows = reinterpret_cast<uint32_t*>(w);
+    a.dd_ent = reinterpret_cast<uint16_t*>(w + (size_t)B * (size_t)Ld * sizeof(uint32_t));
+    a.ws = reinterpret_cast<float*>(w + dd_ws);
+  }
+  a.dd_slab = fmx::bwd_dd_slab((int)d);
   a.sq_n = Nq > 1 ? q_stride_n : 0;
   a.sq_l = q_stride_l;
   a.sd_b = d_stride_b;

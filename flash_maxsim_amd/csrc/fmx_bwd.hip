@@ -134,27 +134,23 @@ __global__ void __launch_bounds__(256) bwd_dq_finalize_kernel(BwdArgs a) {
 }
 
 constexpr int kEntryBits = 13;  // (query, token) entries per doc < 2^13
+constexpr uint32_t kNoRow = 0xffffffffu;
 
-// dD for one doc per workgroup. LDS: the doc's (query, token) entries as keys
-// row << 13 | entry, sorted ascending (bitonic), and a bitmap of picked rows.
-// A picked row's entries are then contiguous and in entry order.
-template <bool BF>
-__device__ __forceinline__ void dd_block(const BwdArgs& a, int b, uint32_t* smem) {
-  uint32_t* keys = smem;
-  uint32_t* hit = smem + a.sort_n;
-  const int nkc = (a.d + 7) >> 3;
+// dD index, one workgroup per doc. The doc's (query, token) entries become
+// keys row << 13 | entry in LDS, bitonic-sorted, so each picked row's entries
+// are contiguous and in entry order. Written to the workspace:
+//   ent[b][p]    entry of sorted position p (uint16), p < Nq*Lq
+//   rows[b][j]   first sorted position | count << 16 of row j, or kNoRow.
+// Docs of length 0 pick no rows.
+__device__ __forceinline__ void dd_index_block(const BwdArgs& a, int b, uint32_t* keys) {
   const int NL = a.Nq * a.Lq;
   const bool empty = a.lengths && doc_len(a, b) == 0;
-  const int nwords = (a.Ld + 31) >> 5;
-  for (int i = threadIdx.x; i < nwords; i += 256) hit[i] = 0u;
-  __syncthreads();
   for (int e = threadIdx.x; e < a.sort_n; e += 256) {
-    uint32_t key = 0xffffffffu;
+    uint32_t key = kNoRow;
     if (e < NL && !empty) {
       const int qi = e / a.Lq, q = e - qi * a.Lq;
       const int j = clamp_index(a.argmax[((int64_t)qi * a.B + b) * a.Lq + q], a.Ld);
       key = ((uint32_t)j << kEntryBits) | (uint32_t)e;
-      atomicOr(&hit[j >> 5], 1u << (j & 31));
     }
     keys[e] = key;
   }
@@ -174,39 +170,79 @@ __device__ __forceinline__ void dd_block(const BwdArgs& a, int b, uint32_t* smem
       __syncthreads();
     }
   }
+  uint16_t* ent = a.dd_ent + (int64_t)b * NL;
+  for (int p = threadIdx.x; p < NL; p += 256) ent[p] = (uint16_t)(keys[p] & ((1u << kEntryBits) - 1));
+  uint32_t* rows = a.dd_rows + (int64_t)b * a.Ld;
+  for (int j = threadIdx.x; j < a.Ld; j += 256) {
+    // first sorted position with row >= j (keys of empty slots are kNoRow)
+    const uint32_t lo_key = (uint32_t)j << kEntryBits;
+    int lo = 0, hi = NL;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (keys[mid] < lo_key) lo = mid + 1; else hi = mid;
+    }
+    uint32_t info = kNoRow;
+    if (lo < NL && (keys[lo] >> kEntryBits) == (uint32_t)j) {
+      int n = 1;
+      while (lo + n < NL && (keys[lo + n] >> kEntryBits) == (uint32_t)j) ++n;
+      info = (uint32_t)lo | ((uint32_t)n << 16);
+    }
+    rows[j] = info;
+  }
+}
 
-  // Rows are dealt to the four waves; a wave's lanes cover a row's 8-wide
-  // k chunks, so each store instruction writes 64 contiguous chunks and all
-  // row/chunk arithmetic is 32-bit without divisions.
-  uint16_t* out = static_cast<uint16_t*>(a.dD) + (int64_t)b * a.Ld * a.d;
+// dD writer: rows of [B, Ld, d] in memory order, a slab of consecutive rows
+// per workgroup, so the stores stream like a fill of the whole tensor. A row
+// no entry picked is zeros; a picked row is the fp32 sum over its entries, in
+// entry order, of g[qi, b] * Q[qi, q]. Lanes cover a row's 8-wide k chunks:
+// L = min(64, pow2 >= chunks) lanes per row, 64 / L rows per wave pass.
+template <bool BF>
+__device__ __forceinline__ void dd_write_block(const BwdArgs& a, int slab) {
+  const int nkc = (a.d + 7) >> 3;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int row = wave; row < a.Ld; row += 4) {
-    if ((hit[row >> 5] >> (row & 31)) & 1u) continue;  // uniform over the wave
-    uint16_t* orow = out + (int64_t)row * a.d;
-    for (int kc = lane; kc < nkc; kc += 64) store8<BF>(orow, kc * 8, a.d, zero);
-  }
-  if (empty) return;
+  int lsh = 0;
+  while ((1 << lsh) < nkc && lsh < 6) ++lsh;
+  const int rpw = 64 >> lsh;               // rows per wave pass
+  const int sub = lane >> lsh;             // this lane's row within the pass
+  const int kc0 = lane & ((1 << lsh) - 1);
+  const int64_t total = (int64_t)a.B * a.Ld;
+  const int64_t r0 = (int64_t)slab * a.dd_slab;
+  const int64_t r1 = r0 + a.dd_slab < total ? r0 + a.dd_slab : total;
+  const int step = 4 * rpw;
+  int64_t r = r0 + wave * rpw + sub;
+  int b = (int)(r / a.Ld);
+  int j = (int)(r - (int64_t)b * a.Ld);
+  const int NL = a.Nq * a.Lq;
   const uint16_t* Q = static_cast<const uint16_t*>(a.Q);
-  for (int p = wave; p < NL; p += 4) {
-    const uint32_t j = keys[p] >> kEntryBits;
-    if (p > 0 && (keys[p - 1] >> kEntryBits) == j) continue;  // not the first entry of its row
-    // The row's entries keys[p .. p2) in entry order, their query rows
-    // weighted by the upstream gradient of (query, doc).
-    for (int kc = lane; kc < nkc; kc += 64) {
-      const int k0 = kc * 8;
-      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int p2 = p; p2 < NL && (keys[p2] >> kEntryBits) == j; ++p2) {
-        const int e = (int)(keys[p2] & ((1u << kEntryBits) - 1));
-        const int qi = e / a.Lq, q = e - qi * a.Lq;
-        const float g = a.grad[(int64_t)qi * a.g_n + (int64_t)b * a.g_b];
-        float x[8];
-        load8<BF>(Q + (int64_t)qi * a.sq_n + (int64_t)q * a.sq_l, k0, a.d, x);
+  const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (; r < r1; r += step) {
+    uint16_t* orow = static_cast<uint16_t*>(a.dD) + r * a.d;
+    const uint32_t info = a.dd_rows[r];
+    if (info == kNoRow) {
+      for (int kc = kc0; kc < nkc; kc += 64) store8<BF>(orow, kc * 8, a.d, zero);
+    } else {
+      const uint16_t* ent = a.dd_ent + (int64_t)b * NL + (info & 0xffffu);
+      const int n = (int)(info >> 16);
+      for (int kc = kc0; kc < nkc; kc += 64) {
+        const int k0 = kc * 8;
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < n; ++i) {
+          const int e = ent[i];
+          const int qi = e / a.Lq, q = e - qi * a.Lq;
+          const float g = a.grad[(int64_t)qi * a.g_n + (int64_t)b * a.g_b];
+          float x[8];
+          load8<BF>(Q + (int64_t)qi * a.sq_n + (int64_t)q * a.sq_l, k0, a.d, x);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) acc[k] = fmaf(g, x[k], acc[k]);
+          for (int k = 0; k < 8; ++k) acc[k] = fmaf(g, x[k], acc[k]);
+        }
+        store8<BF>(orow, k0, a.d, acc);
       }
-      store8<BF>(out + (int64_t)j * a.d, k0, a.d, acc);
+    }
+    j += step;
+    while (j >= a.Ld) {
+      j -= a.Ld;
+      ++b;
     }
   }
 }
@@ -216,10 +252,14 @@ __global__ void __launch_bounds__(256) bwd_dq_partial_kernel(BwdArgs a) {
   dq_partial_block<BF>(a, blockIdx.x, blockIdx.y);
 }
 
-template <bool BF>
-__global__ void __launch_bounds__(256) bwd_dd_kernel(BwdArgs a) {
+__global__ void __launch_bounds__(256) bwd_dd_index_kernel(BwdArgs a) {
   extern __shared__ uint32_t smem[];
-  dd_block<BF>(a, blockIdx.x, smem);
+  dd_index_block(a, blockIdx.x, smem);
+}
+
+template <bool BF>
+__global__ void __launch_bounds__(256) bwd_dd_write_kernel(BwdArgs a) {
+  dd_write_block<BF>(a, blockIdx.x);
 }
 
 // dQ and dD run as separate launches: interleaving the read-bound dQ blocks
@@ -235,8 +275,10 @@ hipError_t launch_bwd_t(const BwdArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(bwd_dq_finalize_kernel<BF>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
   }
   if (a.dD && a.B > 0) {
-    const size_t lds = bwd_dd_lds_bytes((int64_t)a.Nq * a.Lq, a.Ld);
-    hipLaunchKernelGGL(bwd_dd_kernel<BF>, dim3((unsigned)a.B), dim3(256), lds, s, a);
+    const size_t lds = bwd_dd_lds_bytes((int64_t)a.Nq * a.Lq);
+    hipLaunchKernelGGL(bwd_dd_index_kernel, dim3((unsigned)a.B), dim3(256), lds, s, a);
+    const int64_t slabs = ((int64_t)a.B * a.Ld + a.dd_slab - 1) / a.dd_slab;
+    hipLaunchKernelGGL(bwd_dd_write_kernel<BF>, dim3((unsigned)slabs), dim3(256), 0, s, a);
   }
   return hipGetLastError();
 }
@@ -262,8 +304,24 @@ int bwd_sort_n(int64_t entries) {
   return n;
 }
 
-size_t bwd_dd_lds_bytes(int64_t entries, int64_t Ld) {
-  return ((size_t)bwd_sort_n(entries) + (size_t)((Ld + 31) / 32)) * sizeof(uint32_t);
+size_t bwd_dd_lds_bytes(int64_t entries) { return (size_t)bwd_sort_n(entries) * sizeof(uint32_t); }
+
+// Workspace of the dD index: rows [B, Ld] uint32, then ent [B, entries] uint16.
+size_t bwd_dd_index_bytes(int64_t B, int64_t entries, int64_t Ld) {
+  const size_t rows = (size_t)B * (size_t)Ld * sizeof(uint32_t);
+  return rows + (((size_t)B * (size_t)entries * sizeof(uint16_t) + 255) & ~(size_t)255);
+}
+
+// Rows per dD writer workgroup: about 16 KB of output, a whole number of
+// the workgroup's row passes (4 waves x 64 / L rows, L lanes per row).
+int bwd_dd_slab(int d) {
+  const int nkc = (d + 7) / 8;
+  int lsh = 0;
+  while ((1 << lsh) < nkc && lsh < 6) ++lsh;
+  const int pass = 4 * (64 >> lsh);
+  int rows = 16384 / (2 * d);
+  if (rows < pass) rows = pass;
+  return (rows + pass - 1) / pass * pass;
 }
 
 hipError_t launch_bwd(int kind, const BwdArgs& a, hipStream_t s) {

@@ -49,6 +49,9 @@ struct BwdArgs {
   int Nq, B, Lq, Ld, d;
   int nchunk;                 // doc chunks of the dQ gather
   int sort_n;                 // dD: (query, token) entries per doc padded to a power of two
+  uint32_t* dd_rows;          // dD index [B, Ld]: first sorted entry | count << 16, or ~0 (workspace)
+  uint16_t* dd_ent;           // dD index [B, Nq*Lq]: entries of each doc sorted by row (workspace)
+  int dd_slab;                // rows per dD writer workgroup
 };
 
 // Shape class handled by the streaming kernel (query tile in VGPRs, docs read
@@ -122,7 +125,9 @@ hipError_t launch_topk(const TopkArgs& a, hipStream_t s);
 // dQ / dD of the argmax backward.
 int bwd_dq_chunks(int B, int rows, int d);     // rows = Nq * Lq query tokens
 int bwd_sort_n(int64_t entries);               // power of two >= Nq * Lq (>= 64)
-size_t bwd_dd_lds_bytes(int64_t entries, int64_t Ld);  // dynamic LDS of the dD kernel
+size_t bwd_dd_lds_bytes(int64_t entries);      // dynamic LDS of the dD index kernel
+size_t bwd_dd_index_bytes(int64_t B, int64_t entries, int64_t Ld);  // its workspace
+int bwd_dd_slab(int d);                         // rows per dD writer workgroup
 hipError_t launch_bwd(int kind, const BwdArgs& a, hipStream_t s);
 
 }  // namespace fmx

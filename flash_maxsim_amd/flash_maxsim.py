@@ -186,7 +186,7 @@ class _FlashMaxSimFn(torch.autograd.Function):
             if g.dim() == 1:
                 g = g.unsqueeze(0)
             lib = _lib.load()
-            nbytes = lib.fmx_bwd_batched_workspace_bytes(Nq, B, Lq, Ld, d) if need_q else 0
+            nbytes = lib.fmx_bwd_batched_workspace_bytes(Nq, B, Lq, Ld, d)
             ws = _lib.workspace(nbytes, dev)
             with _device_guard(dev):
                 rc = lib.fmx_bwd_batched(

@@ -204,6 +204,12 @@ int fmx_bwd(int dtype, const void* Q, int64_t q_stride_l, const void* D, int64_t
             int64_t B, int64_t Lq, int64_t Ld, int64_t d, void* workspace, size_t workspace_bytes,
             void* stream);
 
+/*
+ * Workspace of fmx_bwd: the dD row index (B*Ld uint32 + B*Lq uint16, when dD
+ * is written) followed by the dQ partial sums (fp32, when dQ is written). The
+ * returned size covers both; a call writing only one of them may pass just
+ * that part.
+ */
 size_t fmx_bwd_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld, int64_t d);
 
 /*
@@ -229,6 +235,7 @@ int fmx_bwd_batched(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stri
                     int64_t Nq, int64_t B, int64_t Lq, int64_t Ld, int64_t d, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* Workspace of fmx_bwd_batched: as fmx_bwd_workspace_bytes with Nq*Lq entries per doc. */
 size_t fmx_bwd_batched_workspace_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t Ld, int64_t d);
 
 #ifdef __cplusplus

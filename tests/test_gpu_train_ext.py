@@ -136,3 +136,20 @@ def test_train_batched_deterministic_and_grad_only_q():
     Qg = Q.clone().requires_grad_(True)
     fm.flash_maxsim_train_batched(Qg, D).sum().backward()
     assert torch.equal(Qg.grad, outs[0][0])
+
+
+@pytest.mark.parametrize("B, Lq, Ld, d", [(5, 24, 37, 20), (3, 16, 300, 2048), (40, 8, 9, 8)])
+def test_train_grad_only_d(oracle_mod, B, Lq, Ld, d):
+    """dD alone (Q without grad) over shapes that exercise the dD writer's
+    row mapping: d % 8 != 0 (scalar stores, 16 rows per wave pass), d = 2048
+    (four passes over a row's chunks) and many tiny docs (slabs spanning docs)."""
+    Q = sim((Lq, d), 1500 + d)
+    D = sim((B, Ld, d), 1501 + d)
+    Dg = D.to(DEV).requires_grad_(True)
+    s = fm.flash_maxsim_train(Q.to(DEV), Dg)
+    g = torch.linspace(0.5, -1.5, B)
+    (s * g.to(DEV)).sum().backward()
+    Qn, Dn = to_np32(Q), to_np32(D)
+    am = saved_argmax(Qn, Dn, None)
+    _, dD_ref = reference_grads(oracle_mod, Qn, Dn, am, g.numpy(), None)
+    np.testing.assert_allclose(Dg.grad.double().cpu().numpy(), dD_ref, rtol=2e-3, atol=ATOL)
