@@ -3,7 +3,7 @@
 // MFMA wrapper, exact uint8 -> fp16 code conversion and wave reductions.
 //
 // Fragment convention of the 16x16x32 form (v_mfma_f32_16x16x32_{f16,bf16}),
-// used by the streaming and split-d kernels:
+// used by every forward kernel:
 //   lane l = 16*g + c   (c = l % 16, g = l / 16)
 //   A operand (16 x 32, M x K): lane l holds row c, k = 8*g .. 8*g+7
 //   B operand (32 x 16, K x N): lane l holds col c, k = 8*g .. 8*g+7
@@ -12,11 +12,9 @@
 // Any permutation of k applied identically to A and B leaves A*B unchanged, so
 // both operands are loaded with the same (row, 32*t + 8*g) addressing.
 //
-// The 32x32x16 form (v_mfma_f32_32x32x16_{f16,bf16}), used by the tiled
-// kernel: lane l = 32*g + c (c = l % 32, g = l / 32) holds row (A) / column
-// (B) c and 8 k values; result register v of lane l is row 8*(v/4) + 4*g + v%4
-// of column c. On gfx950 this form retires twice the flops per cycle of the
-// 16x16x32 form, which is what the MFMA-bound shapes need.
+// The 32x32x16 form (v_mfma_f32_32x32x16_{f16,bf16}): lane l = 32*g + c
+// (c = l % 32, g = l / 32) holds row (A) / column (B) c and 8 k values; result
+// register v of lane l is row 8*(v/4) + 4*g + v%4 of column c.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -155,10 +153,63 @@ __device__ __forceinline__ u32x4_t prefix_mask16(int n) {
   return m;
 }
 
+// Cross-row exchanges on the VALU (no LDS round trip, unlike ds_bpermute):
+// v_permlane16_swap / v_permlane32_swap of a value with itself leave, in
+// every lane l, the value of lane l & ~16 (resp. ~32) in `lo` and that of
+// lane l | 16 (resp. | 32) in `hi`. A commutative combine of lo and hi is the
+// combine of a lane with its partner l ^ 16 (l ^ 32), bitwise equal in both.
+__device__ __forceinline__ void halves16(uint32_t x, uint32_t& lo, uint32_t& hi) {
+  const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  lo = r[0];
+  hi = r[1];
+}
+__device__ __forceinline__ void halves32(uint32_t x, uint32_t& lo, uint32_t& hi) {
+  const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  lo = r[0];
+  hi = r[1];
+}
+__device__ __forceinline__ void halves16(float x, float& lo, float& hi) {
+  uint32_t a, b;
+  halves16(__builtin_bit_cast(uint32_t, x), a, b);
+  lo = __builtin_bit_cast(float, a);
+  hi = __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ void halves32(float x, float& lo, float& hi) {
+  uint32_t a, b;
+  halves32(__builtin_bit_cast(uint32_t, x), a, b);
+  lo = __builtin_bit_cast(float, a);
+  hi = __builtin_bit_cast(float, b);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the 64 lanes of a full wave, the same bits in every lane: within
+// 16-lane rows by DPP (quad xor 1, quad xor 2, half-row mirror, row mirror;
+// each step adds a lane to a partner holding the same partial), then across
+// rows by the permlane swaps.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) v += __shfl_xor(v, s);
-  return v;
+  v += dpp_mov<0xB1>(v);   // quad_perm(1, 0, 3, 2)
+  v += dpp_mov<0x4E>(v);   // quad_perm(2, 3, 0, 1)
+  v += dpp_mov<0x141>(v);  // row_half_mirror
+  v += dpp_mov<0x140>(v);  // row_mirror
+  float lo, hi;
+  halves16(v, lo, hi);
+  v = lo + hi;
+  halves32(v, lo, hi);
+  return lo + hi;
+}
+
+// Running max of a lane's value over the four lanes c, c+16, c+32, c+48 (the
+// four row groups of an MFMA result column), left in every lane.
+__device__ __forceinline__ float max_over_groups(float v) {
+  float lo, hi;
+  halves16(v, lo, hi);
+  v = vmax(lo, hi);
+  halves32(v, lo, hi);
+  return vmax(lo, hi);
 }
 
 // (value, index) max where ties go to the smaller index: combining per-lane
@@ -168,6 +219,24 @@ __device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi)
     v = ov;
     i = oi;
   }
+}
+
+// argmax_merge over the four row groups (lanes c, c+16, c+32, c+48), merged
+// as (group 0 with 1, 2 with 3), then (0-1 with 2-3): the lower group always
+// the first operand. Lanes of group 0 hold the result.
+__device__ __forceinline__ void argmax_over_groups(float& v, int& ix) {
+  float lo, hi;
+  uint32_t ilo, ihi;
+  halves16(v, lo, hi);
+  halves16((uint32_t)ix, ilo, ihi);
+  v = lo;
+  ix = (int)ilo;
+  argmax_merge(v, ix, hi, (int)ihi);
+  halves32(v, lo, hi);
+  halves32((uint32_t)ix, ilo, ihi);
+  v = lo;
+  ix = (int)ilo;
+  argmax_merge(v, ix, hi, (int)ihi);
 }
 
 }  // namespace fmx

@@ -193,15 +193,10 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
   for (int nb = 0; nb < NQB; ++nb) {
     float v = m[nb];
     int ix = mi[nb];
-#pragma unroll
-    for (int s = 16; s <= 32; s <<= 1) {
-      const float ov = __shfl_xor(v, s);
-      if constexpr (ARGMAX) {
-        const int oi = __shfl_xor(ix, s);
-        argmax_merge(v, ix, ov, oi);
-      } else {
-        v = vmax(v, ov);
-      }
+    if constexpr (ARGMAX) {
+      argmax_over_groups(v, ix);
+    } else {
+      v = max_over_groups(v);
     }
     if (g == 0) {
       red_m[wave][nb * 16 + c] = v;

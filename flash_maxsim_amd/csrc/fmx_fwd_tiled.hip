@@ -254,15 +254,10 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
       for (int nb = 0; nb < NB; ++nb) {
         float v = m[nb];
         int ix = mi[nb];
-#pragma unroll
-        for (int sh = 16; sh <= 32; sh <<= 1) {
-          const float ov = __shfl_xor(v, sh);
-          if constexpr (ARGMAX) {
-            const int oi = __shfl_xor(ix, sh);
-            argmax_merge(v, ix, ov, oi);
-          } else {
-            v = vmax(v, ov);
-          }
+        if constexpr (ARGMAX) {
+          argmax_over_groups(v, ix);
+        } else {
+          v = max_over_groups(v);
         }
         if (g == 0) {
           rowmax[par][wave * NB * 16 + nb * 16 + c] = v;
