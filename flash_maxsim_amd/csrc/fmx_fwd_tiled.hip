@@ -117,6 +117,7 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
   const int64_t rows_total = (int64_t)a.Nq * a.Lq;
   const int64_t row0 = (int64_t)rb * R;
   const int64_t row_end = row0 + R < rows_total ? row0 + R : rows_total;
+  const int64_t qfirst = row0 / a.Lq, qlast = (row_end - 1) / a.Lq;  // queries of this row block
 
   // Partial 8-wide group when d % 8 != 0.
   const int kp = a.d & ~7;
@@ -232,14 +233,25 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
         for (int nb = 0; nb < NB; ++nb) fold_rows<ARGMAX>(acc[nb], rowj, len, false, m[nb], mi[nb]);
       }
     } else {
-      // a doc's last, partial tile: skip subtiles past len, mask rows past len
+      // a doc's last, partial tile: its ns subtiles (none for an empty doc)
+      // with the same one-ahead fragment reads, rows past len masked. Each
+      // subtile's MFMAs and fold sit in one block after its branch.
+      // (With the largest row blocks the second fragment buffer does not fit
+      // the register budget; those read each subtile's fragments in turn.)
+      constexpr int AB = NB * KS <= 20 ? 2 : 1;
+      const int ns = len > j0 ? (len - j0 + 15) >> 4 : 0;
+      u32x4_t af[AB][KS];
+      if (AB == 2 && ns > 0) read_frags<KS, ROWB>(af[0], base, 0, c, g);
 #pragma unroll
       for (int s = 0; s < TJ / 16; ++s) {
-        if (j0 + s * 16 < len) {
-          u32x4_t af[KS];
-          read_frags<KS, ROWB>(af, base, s, c, g);
+        if (s < ns) {
+          if (AB == 1) {
+            read_frags<KS, ROWB>(af[0], base, s, c, g);
+          } else if (s + 1 < ns) {
+            read_frags<KS, ROWB>(af[(s + 1) % AB], base, s + 1, c, g);
+          }
           f32x4_t acc[NB];
-          subtile_mfma<BF, NB, KS>(af, qf, acc);
+          subtile_mfma<BF, NB, KS>(af[s % AB], qf, acc);
           const int rowj = j0 + s * 16 + 4 * g;
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) fold_rows<ARGMAX>(acc[nb], rowj, len, true, m[nb], mi[nb]);
@@ -272,7 +284,6 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
 
     if (last) {
       // per-query sums of doc b over this row block
-      const int64_t qfirst = row0 / a.Lq, qlast = (row_end - 1) / a.Lq;
       for (int64_t qi = qfirst + wave; qi <= qlast; qi += NW) {
         const int64_t ra = qi * a.Lq > row0 ? qi * a.Lq : row0;
         const int64_t rz = (qi + 1) * a.Lq < row_end ? (qi + 1) * a.Lq : row_end;
