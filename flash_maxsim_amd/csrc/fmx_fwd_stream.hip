@@ -37,13 +37,18 @@ constexpr int stream_depth() { return 4; }
 
 // KMASK: d is not exactly 32*KS, so fragment slots past d must read as zero.
 // VEC: uint8 vector load path (FwdArgs::vec); true for fp16/bf16.
-template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX, bool VEC>
+// DOCS = 2 (uint8, single query, one pass, no argmax): the workgroup scores docs
+// 2x and 2x+1 as one tile sequence (the first doc's tiles, then the second's),
+// so its query tile, row sums and load ring carry over from one doc to the
+// next instead of being rebuilt and refilled per doc.
+template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX, bool VEC, int DOCS = 1>
 __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
   constexpr int NW = kStreamWaves, P = stream_depth<KIND>(), QROWS = NQB * 16;
   constexpr int ESZ = KindInfo<KIND>::esz;
   constexpr bool BF = KindInfo<KIND>::bf;
   constexpr bool U8 = KIND == KIND_U8;
-  __shared__ float red_m[NW][QROWS];
+  static_assert(DOCS == 1 || (DOCS == 2 && !ARGMAX), "two docs per workgroup: scores only");
+  __shared__ float red_m[DOCS][NW][QROWS];
   __shared__ int red_i[ARGMAX ? NW : 1][QROWS];
 
   const int lane = threadIdx.x & 63;
@@ -51,7 +56,10 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
   const int c = lane & 15, g = lane >> 4;
   const int pass = blockIdx.y;
   int qi, b;
-  if (a.shared_docs && a.Nq > 1) {
+  if constexpr (DOCS == 2) {
+    qi = 0;
+    b = 2 * blockIdx.x;
+  } else if (a.shared_docs && a.Nq > 1) {
     // Queries of one doc run back to back so the doc streams from HBM once
     // and the other queries find it in cache.
     b = blockIdx.x / a.Nq;
@@ -62,9 +70,15 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
   }
   const int item = qi * a.B + b;  // row of argmax / partial, as in the reference
   const int64_t drow = a.shared_docs ? (int64_t)b : (int64_t)item;
-  int len = a.lengths ? a.lengths[drow] : a.Ld;
-  len = len < 0 ? 0 : (len > a.Ld ? a.Ld : len);
-  const int ntiles = (len + 15) >> 4;
+  auto doc_length = [&](int64_t row) {
+    const int l = a.lengths ? a.lengths[row] : a.Ld;
+    return l < 0 ? 0 : (l > a.Ld ? a.Ld : l);
+  };
+  const int len0 = doc_length(drow);
+  const bool two = DOCS == 2 && b + 1 < a.B;  // second doc of the workgroup
+  const int len1 = two ? doc_length(drow + 1) : 0;
+  const int nt0 = (len0 + 15) >> 4;
+  const int ntiles = nt0 + ((len1 + 15) >> 4);  // tile sequence: doc 0's, then doc 1's
   const int my_n = ntiles > wave ? (ntiles - wave + NW - 1) / NW : 0;
 
   // Partial 8-wide group (d % 8 != 0): fragment slot tp of lane group gp.
@@ -99,7 +113,8 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
   }
 
   // ---- doc stream ----
-  const DocRes dr = make_doc_res<KIND, VEC>(a, drow, len);
+  const DocRes dr0 = make_doc_res<KIND, VEC>(a, drow, len0);
+  const DocRes dr1 = DOCS == 2 ? make_doc_res<KIND, VEC>(a, two ? drow + 1 : drow, len1) : dr0;
   uint32_t koff[KS];
 #pragma unroll
   for (int t = 0; t < KS; ++t) {
@@ -107,25 +122,46 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
     // Slots past d read as zeros instead of touching the next row.
     koff[t] = (KMASK && k0 >= a.d) ? kOOB : (uint32_t)(k0 * ESZ);
   }
+  // Sequence position -> (doc, tile of that doc); uniform over the wave.
+  auto seq_load = [&](Tile<KIND, KS>& T, int sq) {
+    if (DOCS == 2 && sq >= nt0) {
+      load_tile<KIND, KS, VEC>(T, dr1, sq - nt0, c, g, koff);
+    } else {
+      load_tile<KIND, KS, VEC>(T, dr0, sq, c, g, koff);
+    }
+  };
 
-  float m[NQB];
+  float m[NQB], m0[NQB];  // running max; m0 holds doc 0's once a wave reaches doc 1
   int mi[NQB];
+  int cur = 0;             // doc of the wave's running max
 #pragma unroll
   for (int nb = 0; nb < NQB; ++nb) {
     m[nb] = -INFINITY;
+    m0[nb] = -INFINITY;
     mi[nb] = 0;
   }
 
   Tile<KIND, KS> buf[P];
 #pragma unroll
   for (int s = 0; s < P; ++s)
-    if (s < my_n) load_tile<KIND, KS, VEC>(buf[s], dr, wave + NW * s, c, g, koff);
+    if (s < my_n) seq_load(buf[s], wave + NW * s);
   for (int i0 = 0; i0 < my_n; i0 += P) {
 #pragma unroll
     for (int s = 0; s < P; ++s) {
       const int i = i0 + s;
       if (i < my_n) {
-        const int tile = wave + NW * i;
+        const int sq = wave + NW * i;
+        const bool in1 = DOCS == 2 && sq >= nt0;
+        const int tile = in1 ? sq - nt0 : sq;
+        const int len = in1 ? len1 : len0;
+        if (DOCS == 2 && in1 && cur == 0) {  // first tile of doc 1 for this wave
+#pragma unroll
+          for (int nb = 0; nb < NQB; ++nb) {
+            m0[nb] = m[nb];
+            m[nb] = -INFINITY;
+          }
+          cur = 1;
+        }
         u32x4_t af[KS];
 #pragma unroll
         for (int t = 0; t < KS; ++t) {
@@ -142,7 +178,7 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
         // The registers of slot s are free once converted: refill them now so
         // the load overlaps this tile's MFMAs. (Loading past the doc instead of
         // branching costs more: those loads still queue behind the real ones.)
-        if (i + P < my_n) load_tile<KIND, KS, VEC>(buf[s], dr, wave + NW * (i + P), c, g, koff);
+        if (i + P < my_n) seq_load(buf[s], wave + NW * (i + P));
         const int row0 = tile * 16 + 4 * g;
         // S of this tile against every query block, folded into the running
         // maxima. TAIL (the doc's last, partial tile) masks rows past len.
@@ -189,32 +225,43 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
   }
 
   // ---- merge the four row groups of each query token, then the four waves ----
+  if (DOCS == 2 && cur == 0) {  // the wave never reached doc 1
 #pragma unroll
-  for (int nb = 0; nb < NQB; ++nb) {
-    float v = m[nb];
-    int ix = mi[nb];
-    if constexpr (ARGMAX) {
-      argmax_over_groups(v, ix);
-    } else {
-      v = max_over_groups(v);
+    for (int nb = 0; nb < NQB; ++nb) {
+      m0[nb] = m[nb];
+      m[nb] = -INFINITY;
     }
-    if (g == 0) {
-      red_m[wave][nb * 16 + c] = v;
-      if constexpr (ARGMAX) red_i[wave][nb * 16 + c] = ix;
+  }
+#pragma unroll
+  for (int dd = 0; dd < DOCS; ++dd) {
+#pragma unroll
+    for (int nb = 0; nb < NQB; ++nb) {
+      float v = (DOCS == 2 && dd == 0) ? m0[nb] : m[nb];
+      int ix = mi[nb];
+      if constexpr (ARGMAX) {
+        argmax_over_groups(v, ix);
+      } else {
+        v = max_over_groups(v);
+      }
+      if (g == 0) {
+        red_m[dd][wave][nb * 16 + c] = v;
+        if constexpr (ARGMAX) red_i[wave][nb * 16 + c] = ix;
+      }
     }
   }
   __syncthreads();
-  if (wave == 0) {
+  const int dd = DOCS == 2 ? wave : 0;  // wave 0 sums doc 0, wave 1 doc 1
+  if (wave < DOCS && (dd == 0 || two)) {
     float part = 0.f;
     for (int r = lane; r < QROWS; r += 64) {
-      float v = red_m[0][r];
+      float v = red_m[dd][0][r];
       int ix = ARGMAX ? red_i[0][r] : 0;
 #pragma unroll
       for (int w = 1; w < NW; ++w) {
         if constexpr (ARGMAX) {
-          argmax_merge(v, ix, red_m[w][r], red_i[w][r]);
+          argmax_merge(v, ix, red_m[0][w][r], red_i[w][r]);
         } else {
-          v = vmax(v, red_m[w][r]);
+          v = vmax(v, red_m[dd][w][r]);
         }
       }
       const int q = q0 + r;
@@ -226,7 +273,7 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
     const float total = wave_sum(part);
     if (lane == 0) {
       if (gridDim.y == 1) {
-        a.scores[(int64_t)qi * a.ss_n + (int64_t)b * a.ss_b] = total;
+        a.scores[(int64_t)qi * a.ss_n + (int64_t)(b + dd) * a.ss_b] = total;
       } else {
         a.partial[(int64_t)pass * gridDim.x + item] = total;  // gridDim.x == Nq*B
       }
@@ -250,6 +297,14 @@ hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
   constexpr int QROWS = NQB * 16;
   const int npass = (a.Lq + QROWS - 1) / QROWS;
   const int64_t items = (int64_t)a.Nq * a.B;
+  if constexpr (KIND == KIND_U8 && !ARGMAX) {
+    // uint8 docs of one query in one pass: two docs per workgroup.
+    if (a.Nq == 1 && npass == 1 && !a.qidx) {
+      hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2>),
+                         dim3((unsigned)((a.B + 1) / 2)), dim3(256), 0, s, a);
+      return hipGetLastError();
+    }
+  }
   hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC>), dim3((unsigned)items, npass),
                      dim3(256), 0, s, a);
   if (npass > 1) {

@@ -251,6 +251,16 @@ def test_int8_long_query(oracle_mod):
     assert_scores(out, ref)
 
 
+@pytest.mark.parametrize("lengths", [[0, 5, 512, 0, 0, 17, 16, 33, 1],
+                                     [512, 0, 16, 15, 0, 0, 300, 511, 64, 65, 2]])
+def test_int8_doc_pairs(oracle_mod, lengths):
+    """Single-query uint8 scoring runs two docs per workgroup: odd doc counts
+    (the last workgroup has one doc), empty docs on either side of a pair, and
+    pairs whose tiles split unevenly over the workgroup's four waves."""
+    out, ref, _ = run_int8(oracle_mod, len(lengths), 32, 512, 128, 360 + len(lengths), lengths=lengths)
+    assert_scores(out, ref)
+
+
 def test_int8_unaligned_scale_rows(oracle_mod):
     """Ld % 4 != 0 makes the kernel read scales one token at a time."""
     out, ref, _ = run_int8(oracle_mod, 7, 32, 301, 128, 350, lengths=[301, 300, 299, 1, 0, 150, 17])
