@@ -42,29 +42,66 @@ constexpr int kTopkThreads = 1024;
 constexpr int kTopkMaxK = 1024;                  // FMX_MAX_TOPK
 constexpr int kTopkC = kTopkThreads * 16;       // keys per chunk (16 per thread)
 
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_or0(int v) {
+  // lanes whose source is outside the pattern (or in a masked row) read 0
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, false);
+}
+
+// Inclusive prefix sum over the 64 lanes of a full wave, all on the VALU:
+// row_shr 1, 2, 4, 8 within each 16-lane row, then row_bcast:15 (rows 1, 3
+// add the last lane of the row below) and row_bcast:31 (rows 2, 3 add lane 31).
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  v += dpp_or0<0x111, 0xf>(v);
+  v += dpp_or0<0x112, 0xf>(v);
+  v += dpp_or0<0x114, 0xf>(v);
+  v += dpp_or0<0x118, 0xf>(v);
+  v += dpp_or0<0x142, 0xa>(v);
+  v += dpp_or0<0x143, 0xc>(v);
+  return v;
+}
+
 __device__ __forceinline__ int block_exclusive_scan(int v, int* wave_tot, int* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int inc = v;
-#pragma unroll
-  for (int s = 1; s < 64; s <<= 1) {
-    const int o = __shfl_up(inc, s);
-    if (lane >= s) inc += o;
-  }
+  const int inc = wave_incl_scan(v);
   if (lane == 63) wave_tot[wave] = inc;
   __syncthreads();
   if (wave == 0) {
-    int t = lane < kTopkThreads / 64 ? wave_tot[lane] : 0;
-    int ti = t;
-#pragma unroll
-    for (int s = 1; s < 16; s <<= 1) {
-      const int o = __shfl_up(ti, s);
-      if (lane >= s) ti += o;
-    }
+    const int t = lane < kTopkThreads / 64 ? wave_tot[lane] : 0;
+    const int ti = wave_incl_scan(t);
     if (lane < kTopkThreads / 64) wave_tot[lane] = ti - t;  // exclusive wave offsets
     if (lane == kTopkThreads / 64 - 1) *total = ti;
   }
   __syncthreads();
   return wave_tot[wave] + inc - v;
+}
+
+// min and max of a 32-bit unsigned value over a full wave (every lane gets both).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ void wave_minmax_u32(uint32_t& mn, uint32_t& mx) {
+  uint32_t a, b;
+#define FMX_MM_STEP(CTRL)                      \
+  a = dpp_u32<CTRL>(mn);                       \
+  b = dpp_u32<CTRL>(mx);                       \
+  mn = a < mn ? a : mn;                        \
+  mx = b > mx ? b : mx;
+  FMX_MM_STEP(0xB1)   // quad_perm(1, 0, 3, 2)
+  FMX_MM_STEP(0x4E)   // quad_perm(2, 3, 0, 1)
+  FMX_MM_STEP(0x141)  // row_half_mirror
+  FMX_MM_STEP(0x140)  // row_mirror
+#undef FMX_MM_STEP
+  uint32_t lo, hi;
+  halves16(mn, lo, hi);
+  mn = lo < hi ? lo : hi;
+  halves16(mx, lo, hi);
+  mx = lo > hi ? lo : hi;
+  halves32(mn, lo, hi);
+  mn = lo < hi ? lo : hi;
+  halves32(mx, lo, hi);
+  mx = lo > hi ? lo : hi;
 }
 
 // grid (chunks, rows). Level 0 (keys_in == null): row r's chunk c covers
@@ -112,30 +149,62 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* s
   uint64_t prefix = 0;
   int shift = 64, krem = want;
   if (want > 0 && want < total) {
-    uint64_t mn = ~(uint64_t)0, mx = 0;
+    // Min and max of the score halves (ord, the upper 32 bits of the keys)
+    // first: when they differ, the smallest and largest keys differ at the
+    // same highest bit. Keys of equal ord need the full 64-bit min and max.
+    uint32_t hmn = 0xffffffffu, hmx = 0u;
 #pragma unroll
     for (int e = 0; e < kTopkE; ++e) {
       if (key[e] != 0) {
-        mn = key[e] < mn ? key[e] : mn;
-        mx = key[e] > mx ? key[e] : mx;
+        const uint32_t h = (uint32_t)(key[e] >> 32);
+        hmn = h < hmn ? h : hmn;
+        hmx = h > hmx ? h : hmx;
       }
     }
-#pragma unroll
-    for (int s = 1; s < 64; s <<= 1) {
-      const uint64_t omn = __shfl_xor(mn, s), omx = __shfl_xor(mx, s);
-      mn = omn < mn ? omn : mn;
-      mx = omx > mx ? omx : mx;
-    }
+    wave_minmax_u32(hmn, hmx);
     if ((tid & 63) == 0) {
-      wmin[tid >> 6] = mn;
-      wmax[tid >> 6] = mx;
+      wmin[tid >> 6] = hmn;
+      wmax[tid >> 6] = hmx;
     }
     __syncthreads();
-    mn = wmin[0];
-    mx = wmax[0];
+    hmn = (uint32_t)wmin[0];
+    hmx = (uint32_t)wmax[0];
     for (int w = 1; w < kTopkThreads / 64; ++w) {
-      mn = wmin[w] < mn ? wmin[w] : mn;
-      mx = wmax[w] > mx ? wmax[w] : mx;
+      hmn = (uint32_t)wmin[w] < hmn ? (uint32_t)wmin[w] : hmn;
+      hmx = (uint32_t)wmax[w] > hmx ? (uint32_t)wmax[w] : hmx;
+    }
+    uint64_t mn, mx;
+    if (hmn != hmx) {
+      mn = (uint64_t)hmn << 32;
+      mx = (uint64_t)hmx << 32;
+    } else {
+      mn = ~(uint64_t)0;
+      mx = 0;
+#pragma unroll
+      for (int e = 0; e < kTopkE; ++e) {
+        if (key[e] != 0) {
+          mn = key[e] < mn ? key[e] : mn;
+          mx = key[e] > mx ? key[e] : mx;
+        }
+      }
+#pragma unroll
+      for (int s = 1; s < 64; s <<= 1) {
+        const uint64_t omn = __shfl_xor(mn, s), omx = __shfl_xor(mx, s);
+        mn = omn < mn ? omn : mn;
+        mx = omx > mx ? omx : mx;
+      }
+      __syncthreads();  // every thread has read the 32-bit wave results
+      if ((tid & 63) == 0) {
+        wmin[tid >> 6] = mn;
+        wmax[tid >> 6] = mx;
+      }
+      __syncthreads();
+      mn = wmin[0];
+      mx = wmax[0];
+      for (int w = 1; w < kTopkThreads / 64; ++w) {
+        mn = wmin[w] < mn ? wmin[w] : mn;
+        mx = wmax[w] > mx ? wmax[w] : mx;
+      }
     }
     shift = 64 - __builtin_clzll(mn ^ mx);  // keys differ only below bit `shift` (mn != mx)
     prefix = shift == 64 ? 0 : mx >> shift;
@@ -160,13 +229,10 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* s
 #pragma unroll
       for (int j = 0; j < 4; ++j) h[j] = hist[4 * tid + j];
       const uint32_t lane_tot = h[0] + h[1] + h[2] + h[3];
-      uint32_t suf = lane_tot;  // sum over lanes >= tid
-#pragma unroll
-      for (int s = 1; s < 64; s <<= 1) {
-        const uint32_t o = __shfl_down(suf, s);
-        if (tid + s < 64) suf += o;
-      }
-      uint32_t above = suf - lane_tot;  // keys in bins of higher lanes
+      // keys in bins of higher lanes: the total minus the inclusive prefix
+      const int incl = wave_incl_scan((int)lane_tot);
+      const uint32_t all = (uint32_t)__builtin_amdgcn_readlane(incl, 63);
+      uint32_t above = all - (uint32_t)incl;
 #pragma unroll
       for (int j = 3; j >= 0; --j) {
         if (above < (uint32_t)krem && (uint32_t)krem <= above + h[j]) {
