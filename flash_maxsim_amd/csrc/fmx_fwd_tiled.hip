@@ -41,11 +41,16 @@ constexpr int kTiledWPC = 8 / kTiledNW;      // two waves per SIMD)
 constexpr int kTileTokens = 64;
 
 // A-fragments of 16-token subtile s from an LDS tile with ROWB-byte rows.
-template <int KS, int ROWB>
+// SWZ: the 16-byte chunk of column j of row r sits at chunk position
+// j ^ (r % 16) (rows unpadded; the 16 rows of a fragment read fall in distinct
+// banks); otherwise at position j of a row padded by 16 bytes.
+template <int KS, int ROWB, bool SWZ>
 __device__ __forceinline__ void read_frags(u32x4_t (&af)[KS], const unsigned char* base, int s, int c, int g) {
 #pragma unroll
-  for (int kk = 0; kk < KS; ++kk)
-    af[kk] = *reinterpret_cast<const u32x4_t*>(base + (s * 16 + c) * ROWB + kk * 64 + g * 16);
+  for (int kk = 0; kk < KS; ++kk) {
+    const int j = kk * 4 + g;
+    af[kk] = *reinterpret_cast<const u32x4_t*>(base + (s * 16 + c) * ROWB + (SWZ ? (j ^ c) : j) * 16);
+  }
 }
 
 // S for one subtile against every query block of the wave; k-step outer so the
@@ -87,14 +92,28 @@ template <int KIND, int NW, int NB, int KS, bool KMASK, bool ARGMAX>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
   constexpr int TJ = kTileTokens;
-  constexpr int ROWB = 64 * KS + 16;       // LDS bytes per token row (16 B pad)
+  // Scores of exact-width rows (no k masking, no argmax) stream global -> LDS
+  // with buffer loads that write LDS directly (16 bytes per lane, one 1 KB run
+  // per wave instruction), into a chunk-swizzled layout. Rows with masked k
+  // chunks, and the argmax instances (whose registers do not fit the twice
+  // unrolled tile loop the DMA path needs), stage through VGPRs into
+  // 16-byte-padded rows.
+  constexpr bool DMA = !KMASK && !ARGMAX;
+  constexpr int ROWB = 64 * KS + (DMA ? 0 : 16);  // LDS bytes per token row
   constexpr int BUFB = TJ * ROWB;          // LDS bytes per tile buffer
   constexpr int CPR = 4 * KS;              // 16-byte chunks per token row
   constexpr int CPT = TJ * CPR / (NW * 64);  // chunks per thread per tile
   constexpr int R = NW * NB * 16;          // rows per row block
   constexpr bool BF = KindInfo<KIND>::bf;
   static_assert(CPT * NW * 64 == TJ * CPR, "tile must split evenly over the workgroup");
-  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * BUFB];
+  // Two tile buffers as separate arrays. On the DMA path each is named at
+  // compile time in the twice unrolled tile loop: the compiler then sees that
+  // a ds_read of one buffer cannot alias the DMA writes in flight to the
+  // other, and places no wait for those writes in front of it.
+  // The staging path keeps both buffers in one array indexed at run time.
+  __shared__ __attribute__((aligned(16))) unsigned char lds0[DMA ? BUFB : 16];
+  __shared__ __attribute__((aligned(16))) unsigned char lds1[DMA ? BUFB : 16];
+  __shared__ __attribute__((aligned(16))) unsigned char ldsa[DMA ? 16 : 2 * BUFB];
   __shared__ float rowmax[2][R];
   __shared__ int rowidx[ARGMAX ? 2 : 1][ARGMAX ? R : 1];
 
@@ -174,13 +193,30 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
       if (has_partial && e0 == kp) stage[k] &= prefix_mask16(a.d & 7);
     }
   };
-  auto store_tile_lds = [&](int buf) {
+  auto store_tile_lds = [&](unsigned char* dst) {
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int chunk = tid + k * NW * 64;
       const int row = chunk / CPR, cc = chunk - (chunk / CPR) * CPR;
-      *reinterpret_cast<u32x4_t*>(lds + buf * BUFB + row * ROWB + cc * 16) = stage[k];
+      *reinterpret_cast<u32x4_t*>(dst + row * ROWB + cc * 16) = stage[k];
     }
+  };
+  // DMA: instruction k of wave w fills chunk positions (k*NW + w)*64 .. +63 of
+  // the buffer; lane l's position holds column (position % CPR) ^ (row % 16).
+  auto dma_tile = [&](rsrc_t rd, int t, unsigned char* dst) {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int slot = (k * NW + wave) * 64 + lane;
+      const int row = slot / CPR, pos = slot - (slot / CPR) * CPR;
+      const int col = pos ^ (row & 15);
+      const uint32_t off = (uint32_t)(t * TJ + row) * rowb + (uint32_t)(col * 16);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rd, (__attribute__((address_space(3))) void*)(dst + (k * NW + wave) * 1024), 16, off, 0, 0, 0);
+    }
+  };
+  // Every wave's DMA writes of the next tile are in LDS before the barrier.
+  auto dma_wait = [&]() {
+    if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
   };
 
   float m[NB];
@@ -196,11 +232,17 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
   int len = doc_len(b);
   int nt = len > 0 ? (len + TJ - 1) / TJ : 1;  // an empty doc still takes one fully masked tile
   rsrc_t rd = tile_rsrc(b, len);
-  load_tile_regs(rd, 0);
-  store_tile_lds(0);
+  if constexpr (DMA) {
+    dma_tile(rd, 0, lds0);
+    dma_wait();
+  } else {
+    load_tile_regs(rd, 0);
+    store_tile_lds(ldsa);
+  }
   __syncthreads();
-  int buf = 0, t = 0, par = 0;
-  while (true) {
+  int t = 0, par = 0;
+  // One tile: compute from buffer cur while the next tile fills nxt.
+  auto step = [&](unsigned char* const cur, unsigned char* const nxt) __attribute__((always_inline)) -> bool {
     int nb_doc = b, nt_tile = t + 1, nlen = len;
     if (nt_tile >= nt) {
       nb_doc = b + G;
@@ -213,19 +255,23 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
         nlen = doc_len(nb_doc);
         rd_next = tile_rsrc(nb_doc, nlen);
       }
-      load_tile_regs(rd_next, nt_tile);
+      if constexpr (DMA) {
+        dma_tile(rd_next, nt_tile, nxt);  // nxt was last read before the previous barrier
+      } else {
+        load_tile_regs(rd_next, nt_tile);
+      }
     }
 
-    // compute tile t of doc b from lds[buf]
+    // compute tile t of doc b from the current buffer
     const int j0 = t * TJ;
-    const unsigned char* base = lds + buf * BUFB;
+    const unsigned char* base = cur;
     if (j0 + TJ <= len) {
       // full tile: branch-free, A-fragments of subtile s+1 read while s computes
       u32x4_t af[2][KS];
-      read_frags<KS, ROWB>(af[0], base, 0, c, g);
+      read_frags<KS, ROWB, DMA>(af[0], base, 0, c, g);
 #pragma unroll
       for (int s = 0; s < TJ / 16; ++s) {
-        if (s + 1 < TJ / 16) read_frags<KS, ROWB>(af[(s + 1) & 1], base, s + 1, c, g);
+        if (s + 1 < TJ / 16) read_frags<KS, ROWB, DMA>(af[(s + 1) & 1], base, s + 1, c, g);
         f32x4_t acc[NB];
         subtile_mfma<BF, NB, KS>(af[s & 1], qf, acc);
         const int rowj = j0 + s * 16 + 4 * g;
@@ -241,14 +287,14 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
       constexpr int AB = NB * KS <= 20 ? 2 : 1;
       const int ns = len > j0 ? (len - j0 + 15) >> 4 : 0;
       u32x4_t af[AB][KS];
-      if (AB == 2 && ns > 0) read_frags<KS, ROWB>(af[0], base, 0, c, g);
+      if (AB == 2 && ns > 0) read_frags<KS, ROWB, DMA>(af[0], base, 0, c, g);
 #pragma unroll
       for (int s = 0; s < TJ / 16; ++s) {
         if (s < ns) {
           if (AB == 1) {
-            read_frags<KS, ROWB>(af[0], base, s, c, g);
+            read_frags<KS, ROWB, DMA>(af[0], base, s, c, g);
           } else if (s + 1 < ns) {
-            read_frags<KS, ROWB>(af[(s + 1) % AB], base, s + 1, c, g);
+            read_frags<KS, ROWB, DMA>(af[(s + 1) % AB], base, s + 1, c, g);
           }
           f32x4_t acc[NB];
           subtile_mfma<BF, NB, KS>(af[s % AB], qf, acc);
@@ -279,7 +325,11 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
         mi[nb] = 0;
       }
     }
-    if (has_next) store_tile_lds(buf ^ 1);
+    if constexpr (DMA) {
+      dma_wait();
+    } else {
+      if (has_next) store_tile_lds(nxt);
+    }
     __syncthreads();
 
     if (last) {
@@ -304,7 +354,7 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
       }
       par ^= 1;
     }
-    if (!has_next) break;
+    if (!has_next) return false;
     if (nb_doc != b) {
       b = nb_doc;
       len = nlen;
@@ -312,7 +362,128 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
       rd = rd_next;
     }
     t = nt_tile;
-    buf ^= 1;
+    return true;
+  };
+  if constexpr (DMA) {
+    while (step(lds0, lds1) && step(lds1, lds0)) {
+    }
+  } else {
+    // staging path: the tile loop as a plain loop over a run-time buffer index
+    int buf = 0;
+    while (true) {
+      int nb_doc = b, nt_tile = t + 1, nlen = len;
+      if (nt_tile >= nt) {
+        nb_doc = b + G;
+        nt_tile = 0;
+      }
+      const bool has_next = nb_doc < a.B;
+      rsrc_t rd_next = rd;
+      if (has_next) {
+        if (nb_doc != b) {
+          nlen = doc_len(nb_doc);
+          rd_next = tile_rsrc(nb_doc, nlen);
+        }
+        load_tile_regs(rd_next, nt_tile);
+      }
+
+      // compute tile t of doc b from lds[buf]
+      const int j0 = t * TJ;
+      const unsigned char* base = ldsa + buf * BUFB;
+      if (j0 + TJ <= len) {
+        // full tile: branch-free, A-fragments of subtile s+1 read while s computes
+        u32x4_t af[2][KS];
+        read_frags<KS, ROWB, false>(af[0], base, 0, c, g);
+  #pragma unroll
+        for (int s = 0; s < TJ / 16; ++s) {
+          if (s + 1 < TJ / 16) read_frags<KS, ROWB, false>(af[(s + 1) & 1], base, s + 1, c, g);
+          f32x4_t acc[NB];
+          subtile_mfma<BF, NB, KS>(af[s & 1], qf, acc);
+          const int rowj = j0 + s * 16 + 4 * g;
+  #pragma unroll
+          for (int nb = 0; nb < NB; ++nb) fold_rows<ARGMAX>(acc[nb], rowj, len, false, m[nb], mi[nb]);
+        }
+      } else {
+        // a doc's last, partial tile: its ns subtiles (none for an empty doc)
+        // with the same one-ahead fragment reads, rows past len masked. Each
+        // subtile's MFMAs and fold sit in one block after its branch.
+        // (With the largest row blocks the second fragment buffer does not fit
+        // the register budget; those read each subtile's fragments in turn.)
+        constexpr int AB = NB * KS <= 20 ? 2 : 1;
+        const int ns = len > j0 ? (len - j0 + 15) >> 4 : 0;
+        u32x4_t af[AB][KS];
+        if (AB == 2 && ns > 0) read_frags<KS, ROWB, false>(af[0], base, 0, c, g);
+  #pragma unroll
+        for (int s = 0; s < TJ / 16; ++s) {
+          if (s < ns) {
+            if (AB == 1) {
+              read_frags<KS, ROWB, false>(af[0], base, s, c, g);
+            } else if (s + 1 < ns) {
+              read_frags<KS, ROWB, false>(af[(s + 1) % AB], base, s + 1, c, g);
+            }
+            f32x4_t acc[NB];
+            subtile_mfma<BF, NB, KS>(af[s % AB], qf, acc);
+            const int rowj = j0 + s * 16 + 4 * g;
+  #pragma unroll
+            for (int nb = 0; nb < NB; ++nb) fold_rows<ARGMAX>(acc[nb], rowj, len, true, m[nb], mi[nb]);
+          }
+        }
+      }
+
+      const bool last = t + 1 >= nt;
+      if (last) {
+        // row maxima of doc b -> rowmax[par]
+  #pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          float v = m[nb];
+          int ix = mi[nb];
+          if constexpr (ARGMAX) {
+            argmax_over_groups(v, ix);
+          } else {
+            v = max_over_groups(v);
+          }
+          if (g == 0) {
+            rowmax[par][wave * NB * 16 + nb * 16 + c] = v;
+            if constexpr (ARGMAX) rowidx[par][wave * NB * 16 + nb * 16 + c] = ix;
+          }
+          m[nb] = -INFINITY;
+          mi[nb] = 0;
+        }
+      }
+      if (has_next) store_tile_lds(ldsa + (buf ^ 1) * BUFB);
+      __syncthreads();
+
+      if (last) {
+        // per-query sums of doc b over this row block
+        for (int64_t qi = qfirst + wave; qi <= qlast; qi += NW) {
+          const int64_t ra = qi * a.Lq > row0 ? qi * a.Lq : row0;
+          const int64_t rz = (qi + 1) * a.Lq < row_end ? (qi + 1) * a.Lq : row_end;
+          float sum = 0.f;
+          for (int64_t r = ra + lane; r < rz; r += 64) {
+            sum += rowmax[par][r - row0];
+            if constexpr (ARGMAX) a.argmax[(qi * a.B + b) * a.Lq + (r - qi * a.Lq)] = rowidx[par][r - row0];
+          }
+          sum = wave_sum(sum);
+          if (lane == 0) {
+            const bool whole = ra == qi * a.Lq && rz == (qi + 1) * a.Lq;
+            if (whole) {
+              a.scores[qi * a.ss_n + (int64_t)b * a.ss_b] = sum;
+            } else {
+              a.partial[(int64_t)rb * a.Nq * a.B + qi * a.B + b] = sum;
+            }
+          }
+        }
+        par ^= 1;
+      }
+      if (!has_next) break;
+      if (nb_doc != b) {
+        b = nb_doc;
+        len = nlen;
+        nt = len > 0 ? (len + TJ - 1) / TJ : 1;
+        rd = rd_next;
+      }
+      t = nt_tile;
+      buf ^= 1;
+    }
   }
 }
 
