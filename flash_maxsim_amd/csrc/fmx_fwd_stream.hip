@@ -123,12 +123,21 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
     koff[t] = (KMASK && k0 >= a.d) ? kOOB : (uint32_t)(k0 * ESZ);
   }
   // Sequence position -> (doc, tile of that doc); uniform over the wave.
+  // Positions past the sequence read an empty range (zeros, no memory access).
+  constexpr bool FIXED = U8;  // fixed load pattern (below)
+  const rsrc_t nul = make_rsrc(a.D, 0u);
   auto seq_load = [&](Tile<KIND, KS>& T, int sq) {
-    if (DOCS == 2 && sq >= nt0) {
-      load_tile<KIND, KS, VEC>(T, dr1, sq - nt0, c, g, koff);
-    } else {
-      load_tile<KIND, KS, VEC>(T, dr0, sq, c, g, koff);
-    }
+    const bool past = FIXED && sq >= ntiles;
+    const bool in1 = DOCS == 2 && sq >= nt0;
+    // Selects over values: a conditional over the DocRes structs themselves
+    // selects their addresses and moves them to scratch memory.
+    const rsrc_t d0 = dr0.d, d1 = dr1.d, s0 = dr0.s, s1 = dr1.s, n0 = dr0.m, n1 = dr1.m;
+    DocRes r;
+    r.d = past ? nul : (in1 ? d1 : d0);
+    r.s = past ? nul : (in1 ? s1 : s0);
+    r.m = past ? nul : (in1 ? n1 : n0);
+    r.rowb = dr0.rowb;
+    load_tile<KIND, KS, VEC>(T, r, past ? 0 : (in1 ? sq - nt0 : sq), c, g, koff);
   };
 
   float m[NQB], m0[NQB];  // running max; m0 holds doc 0's once a wave reaches doc 1
@@ -141,86 +150,116 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
     mi[nb] = 0;
   }
 
-  Tile<KIND, KS> buf[P];
+  // Tile i of the wave's sequence from ring slot T. The slot's refill (tile
+  // i + P) is issued after the operands are taken and before the MFMAs:
+  // REFILL_ANY loads it whether or not it exists (past the end: the empty
+  // range), REFILL_IF only if it exists, REFILL_NONE not at all.
+  enum { REFILL_NONE, REFILL_IF, REFILL_ANY };
+  auto process = [&](auto mode_tag, Tile<KIND, KS>& T, int i) __attribute__((always_inline)) {
+    constexpr int MODE = decltype(mode_tag)::value;
+    const int sq = wave + NW * i;
+    const bool in1 = DOCS == 2 && sq >= nt0;
+    const int tile = in1 ? sq - nt0 : sq;
+    const int len = in1 ? len1 : len0;
+    if (DOCS == 2 && in1 && cur == 0) {  // first tile of doc 1 for this wave
 #pragma unroll
-  for (int s = 0; s < P; ++s)
-    if (s < my_n) seq_load(buf[s], wave + NW * s);
-  for (int i0 = 0; i0 < my_n; i0 += P) {
+      for (int nb = 0; nb < NQB; ++nb) {
+        m0[nb] = m[nb];
+        m[nb] = -INFINITY;
+      }
+      cur = 1;
+    }
+    u32x4_t af[KS];
 #pragma unroll
-    for (int s = 0; s < P; ++s) {
-      const int i = i0 + s;
-      if (i < my_n) {
-        const int sq = wave + NW * i;
-        const bool in1 = DOCS == 2 && sq >= nt0;
-        const int tile = in1 ? sq - nt0 : sq;
-        const int len = in1 ? len1 : len0;
-        if (DOCS == 2 && in1 && cur == 0) {  // first tile of doc 1 for this wave
+    for (int t = 0; t < KS; ++t) {
+      af[t] = tile_operand<KIND, KS>(T, t);
+      if constexpr (KMASK && !U8) {
+        if (has_partial && t == tp) af[t] &= pmask;
+      }
+    }
+    float sc[4], off[4];
+    if constexpr (U8) {
 #pragma unroll
-          for (int nb = 0; nb < NQB; ++nb) {
-            m0[nb] = m[nb];
-            m[nb] = -INFINITY;
-          }
-          cur = 1;
-        }
-        u32x4_t af[KS];
+      for (int r = 0; r < 4; ++r) tile_affine(T.s, T.m, r, sc[r], off[r]);
+    }
+    // uint8 codes were converted into registers of their own, so the slot is
+    // free; fp16/bf16 MFMAs read the slot itself (the compiler keeps a copy).
+    if constexpr (MODE == REFILL_ANY) seq_load(T, wave + NW * (i + P));
+    if constexpr (MODE == REFILL_IF) {
+      if (i + P < my_n) seq_load(T, wave + NW * (i + P));
+    }
+    const int row0 = tile * 16 + 4 * g;
+    // S of this tile against every query block, folded into the running
+    // maxima. TAIL (the doc's last, partial tile) masks rows past len.
+    // The two instances are chosen by a branch before the MFMAs, so each
+    // keeps its MFMAs and the first VALU reads of their results in one
+    // basic block: the compiler inserts the MFMA-to-VALU wait states within
+    // a block, and a branch between the two (a conditional mask after the
+    // MFMAs) let it place the reads too early.
+    auto score_tile = [&](auto tail_tag) __attribute__((always_inline)) {
+      constexpr bool TAIL = decltype(tail_tag)::value;
 #pragma unroll
-        for (int t = 0; t < KS; ++t) {
-          af[t] = tile_operand<KIND, KS>(buf[s], t);
-          if constexpr (KMASK && !U8) {
-            if (has_partial && t == tp) af[t] &= pmask;
-          }
-        }
-        float sc[4], off[4];
+      for (int nb = 0; nb < NQB; ++nb) {
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < KS; ++t) acc = mfma16x16x32<BF>(af[t], qf[nb][t], acc);
         if constexpr (U8) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) tile_affine(buf[s].s, buf[s].m, r, sc[r], off[r]);
+          for (int r = 0; r < 4; ++r) acc[r] = fmaf(sc[r], acc[r], off[r] * qsum[nb]);
         }
-        // The registers of slot s are free once converted: refill them now so
-        // the load overlaps this tile's MFMAs. (Loading past the doc instead of
-        // branching costs more: those loads still queue behind the real ones.)
-        if (i + P < my_n) seq_load(buf[s], wave + NW * (i + P));
-        const int row0 = tile * 16 + 4 * g;
-        // S of this tile against every query block, folded into the running
-        // maxima. TAIL (the doc's last, partial tile) masks rows past len.
-        // The two instances are chosen by a branch before the MFMAs, so each
-        // keeps its MFMAs and the first VALU reads of their results in one
-        // basic block: the compiler inserts the MFMA-to-VALU wait states within
-        // a block, and a branch between the two (a conditional mask after the
-        // MFMAs) let it place the reads too early.
-        auto score_tile = [&](auto tail_tag) {
-          constexpr bool TAIL = decltype(tail_tag)::value;
+        if constexpr (TAIL) {
 #pragma unroll
-          for (int nb = 0; nb < NQB; ++nb) {
-            f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+          for (int r = 0; r < 4; ++r) acc[r] = row0 + r < len ? acc[r] : -INFINITY;
+        }
+        if constexpr (ARGMAX) {
 #pragma unroll
-            for (int t = 0; t < KS; ++t) acc = mfma16x16x32<BF>(af[t], qf[nb][t], acc);
-            if constexpr (U8) {
-#pragma unroll
-              for (int r = 0; r < 4; ++r) acc[r] = fmaf(sc[r], acc[r], off[r] * qsum[nb]);
-            }
-            if constexpr (TAIL) {
-#pragma unroll
-              for (int r = 0; r < 4; ++r) acc[r] = row0 + r < len ? acc[r] : -INFINITY;
-            }
-            if constexpr (ARGMAX) {
-#pragma unroll
-              for (int r = 0; r < 4; ++r) {
-                if (acc[r] > m[nb]) {
-                  m[nb] = acc[r];
-                  mi[nb] = row0 + r;
-                }
-              }
-            } else {
-              m[nb] = fold_max4(m[nb], acc[0], acc[1], acc[2], acc[3]);
+          for (int r = 0; r < 4; ++r) {
+            if (acc[r] > m[nb]) {
+              m[nb] = acc[r];
+              mi[nb] = row0 + r;
             }
           }
-        };
-        if (tile * 16 + 16 > len) {
-          score_tile(std::true_type{});
         } else {
-          score_tile(std::false_type{});
+          m[nb] = fold_max4(m[nb], acc[0], acc[1], acc[2], acc[3]);
         }
       }
+    };
+    if (tile * 16 + 16 > len) {
+      score_tile(std::true_type{});
+    } else {
+      score_tile(std::false_type{});
+    }
+  };
+  using RefillNone = std::integral_constant<int, REFILL_NONE>;
+  using RefillIf = std::integral_constant<int, REFILL_IF>;
+  using RefillAny = std::integral_constant<int, REFILL_ANY>;
+
+  Tile<KIND, KS> buf[P];
+  if constexpr (FIXED) {
+    // A fixed load pattern: every group of P tiles that has a next group
+    // refills all P slots, so the compiler's wait before each tile counts the
+    // P-1 tiles still in flight behind it (a conditional load makes it wait
+    // for all of them). The empty-range loads past the end cost issue slots;
+    // fp16/bf16 waves (4-5 tiles each at config 1) lose more to those than
+    // they gain, uint8 waves (two docs, ~16 tiles) gain.
+#pragma unroll
+    for (int s = 0; s < P; ++s) seq_load(buf[s], wave + NW * s);
+    int i0 = 0;
+    for (; i0 + P < my_n; i0 += P) {
+#pragma unroll
+      for (int s = 0; s < P; ++s) process(RefillAny{}, buf[s], i0 + s);
+    }
+#pragma unroll
+    for (int s = 0; s < P; ++s)
+      if (i0 + s < my_n) process(RefillNone{}, buf[s], i0 + s);
+  } else {
+#pragma unroll
+    for (int s = 0; s < P; ++s)
+      if (s < my_n) seq_load(buf[s], wave + NW * s);
+    for (int i0 = 0; i0 < my_n; i0 += P) {
+#pragma unroll
+      for (int s = 0; s < P; ++s)
+        if (i0 + s < my_n) process(RefillIf{}, buf[s], i0 + s);
     }
   }
 
