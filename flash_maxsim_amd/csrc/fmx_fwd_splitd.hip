@@ -147,54 +147,86 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
   // after every owner passed tile t+1's barrier, i.e. finished reducing t.
   Tile<KIND, KSW> buf[P];
   float psc[4] = {0.f, 0.f, 0.f, 0.f}, poff[4] = {0.f, 0.f, 0.f, 0.f};  // tile t-1 (uint8 docs)
+  // Tile `tile` from ring slot T. Its slot's refill (tile + P) is issued
+  // after the MFMAs have taken the operands (so they need no copy of their
+  // own): REFILL_ANY whether or not that tile exists (past the doc it reads
+  // zeros), REFILL_IF only if it does, REFILL_NONE not at all.
+  enum { REFILL_NONE, REFILL_IF, REFILL_ANY };
+  auto process = [&](auto mode_tag, Tile<KIND, KSW>& T, int tile) __attribute__((always_inline)) {
+    constexpr int MODE = decltype(mode_tag)::value;
+    u32x4_t af[KSW];
 #pragma unroll
-  for (int s = 0; s < P; ++s)
-    if (s < ntiles) load_tile<KIND, KSW, VEC>(buf[s], dr, s, c, g, koff);
-  for (int i0 = 0; i0 < ntiles; i0 += P) {
-#pragma unroll
-    for (int s = 0; s < P; ++s) {
-      const int tile = i0 + s;
-      if (tile < ntiles) {  // uniform over the workgroup: the barriers below are safe
-        u32x4_t af[KSW];
-#pragma unroll
-        for (int t = 0; t < KSW; ++t) {
-          af[t] = tile_operand<KIND, KSW>(buf[s], t);
-          if constexpr (KMASK && !U8) {
-            if (has_partial && t == tp) af[t] &= pmask;
-          }
-        }
-        float sc[4], off[4];
-        if constexpr (U8) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) tile_affine(buf[s].s, buf[s].m, r, sc[r], off[r]);
-        }
-        f32x4_t acc[NQB];
-#pragma unroll
-        for (int nb = 0; nb < NQB; ++nb) {
-          acc[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int t = 0; t < KSW; ++t) acc[nb] = mfma16x16x32<BF>(af[t], qf[nb][t], acc[nb]);
-        }
-        // Refill slot s after the MFMAs have taken its operands, so the
-        // operands need no copy of their own.
-        if (tile + P < ntiles) load_tile<KIND, KSW, VEC>(buf[s], dr, tile + P, c, g, koff);
-        // The first half of the query blocks finished first: store them, then
-        // reduce the previous tile while the second half runs.
-        constexpr int H = NQB / 2;
-#pragma unroll
-        for (int nb = 0; nb < H; ++nb) part[tile & 1][wave][nb][lane] = acc[nb];
-        if (tile > 0) reduce_tile(tile - 1, psc, poff);
-#pragma unroll
-        for (int nb = H; nb < NQB; ++nb) part[tile & 1][wave][nb][lane] = acc[nb];
-        if constexpr (U8) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            psc[r] = sc[r];
-            poff[r] = off[r];
-          }
-        }
-        __syncthreads();
+    for (int t = 0; t < KSW; ++t) {
+      af[t] = tile_operand<KIND, KSW>(T, t);
+      if constexpr (KMASK && !U8) {
+        if (has_partial && t == tp) af[t] &= pmask;
       }
+    }
+    float sc[4], off[4];
+    if constexpr (U8) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) tile_affine(T.s, T.m, r, sc[r], off[r]);
+    }
+    f32x4_t acc[NQB];
+#pragma unroll
+    for (int nb = 0; nb < NQB; ++nb) {
+      acc[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < KSW; ++t) acc[nb] = mfma16x16x32<BF>(af[t], qf[nb][t], acc[nb]);
+    }
+    if constexpr (MODE == REFILL_ANY) load_tile<KIND, KSW, VEC>(T, dr, tile + P, c, g, koff);
+    if constexpr (MODE == REFILL_IF) {
+      if (tile + P < ntiles) load_tile<KIND, KSW, VEC>(T, dr, tile + P, c, g, koff);
+    }
+    // The first half of the query blocks finished first: store them, then
+    // reduce the previous tile while the second half runs.
+    constexpr int H = NQB / 2;
+#pragma unroll
+    for (int nb = 0; nb < H; ++nb) part[tile & 1][wave][nb][lane] = acc[nb];
+    if (tile > 0) reduce_tile(tile - 1, psc, poff);
+#pragma unroll
+    for (int nb = H; nb < NQB; ++nb) part[tile & 1][wave][nb][lane] = acc[nb];
+    if constexpr (U8) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        psc[r] = sc[r];
+        poff[r] = off[r];
+      }
+    }
+    __syncthreads();
+  };
+  using RefillNone = std::integral_constant<int, REFILL_NONE>;
+  using RefillIf = std::integral_constant<int, REFILL_IF>;
+  using RefillAny = std::integral_constant<int, REFILL_ANY>;
+  // ntiles is uniform over the workgroup, so the barriers inside are safe.
+  // FIXED: a fixed load pattern. The first P tiles are loaded, and every group
+  // of P tiles that has a successor refills all P slots; tiles past the doc
+  // read zeros from outside its buffer range without touching memory. The
+  // compiler's wait before each tile then counts the tiles still in flight
+  // behind it, where a conditional load makes it wait for all of them (a full
+  // drain every other tile at P = 2). The largest masked instances keep
+  // conditional loads (the fixed pattern's extra registers spill there), and
+  // so do uint8 rows without 16-byte alignment (one wave per SIMD fewer).
+  constexpr bool FIXED = VEC && !(KMASK && NQB * KSW >= 32);
+  if constexpr (FIXED) {
+#pragma unroll
+    for (int s = 0; s < P; ++s) load_tile<KIND, KSW, VEC>(buf[s], dr, s, c, g, koff);
+    int i0 = 0;
+    for (; i0 + P < ntiles; i0 += P) {
+#pragma unroll
+      for (int s = 0; s < P; ++s) process(RefillAny{}, buf[s], i0 + s);
+    }
+#pragma unroll
+    for (int s = 0; s < P; ++s)
+      if (i0 + s < ntiles) process(RefillNone{}, buf[s], i0 + s);
+  } else {
+#pragma unroll
+    for (int s = 0; s < P; ++s)
+      if (s < ntiles) load_tile<KIND, KSW, VEC>(buf[s], dr, s, c, g, koff);
+    for (int i0 = 0; i0 < ntiles; i0 += P) {
+#pragma unroll
+      for (int s = 0; s < P; ++s)
+        if (i0 + s < ntiles) process(RefillIf{}, buf[s], i0 + s);
     }
   }
   if (ntiles > 0) reduce_tile(ntiles - 1, psc, poff);
