@@ -7,7 +7,9 @@
 // One workgroup of four waves scores one (query, doc) pair for one pass of up
 // to 16*NQB query tokens:
 //  * the pass's query tile (16*NQB tokens x 32*KS dims) sits in VGPRs as MFMA
-//    B-fragments for the whole doc;
+//    B-fragments for the whole doc; the workgroup loads it once (each wave a
+//    quarter of the fragments, exchanged through LDS while the first doc
+//    tiles are in flight);
 //  * the doc's 16-token tiles are dealt round-robin to the four waves, which
 //    load them with 128-bit (fp16/bf16) or 64-bit (uint8) buffer loads straight
 //    into VGPRs, P tiles deep, so no LDS round trip sits on the HBM stream;
@@ -91,26 +93,47 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
   // ---- query tile of this pass (B operand) ----
   const int q0 = pass * QROWS;
   const rsrc_t rq = make_rsrc((const char*)a.Q + (int64_t)qi * a.sq_n * 2, (uint32_t)(a.Lq_rows * a.sq_l * 2));
-  u32x4_t qf[NQB][KS];
-  float qsum[NQB];
+  // Each wave loads every NW-th fragment of the query tile; the fragments
+  // meet in LDS once the first doc tiles are in flight (q_exchange), so the
+  // workgroup issues the query loads once instead of once per wave.
+  constexpr int NF = NQB * KS, FPW = (NF + NW - 1) / NW;
+  __shared__ u32x4_t qs[NF][64];
+  u32x4_t qv[FPW];
 #pragma unroll
-  for (int nb = 0; nb < NQB; ++nb) {
-    const uint32_t rowoff = query_row_offset(a, b, q0 + nb * 16 + c);
-#pragma unroll
-    for (int t = 0; t < KS; ++t) {
+  for (int j = 0; j < FPW; ++j) {
+    const int f = wave + NW * j;
+    qv[j] = u32x4_t{0u, 0u, 0u, 0u};
+    if (f < NF) {
+      const int nb = f / KS, t = f - (f / KS) * KS;
+      const uint32_t rowoff = query_row_offset(a, b, q0 + nb * 16 + c);
       const int k0 = frag_k0<KIND>(t, g);
       if constexpr (KMASK) {
-        qf[nb][t] = ld16(rq, k0 < a.d ? rowoff + (uint32_t)(k0 * 2) : kOOB);
-        if (has_partial && t == tp) qf[nb][t] &= pmask;
+        qv[j] = ld16(rq, k0 < a.d ? rowoff + (uint32_t)(k0 * 2) : kOOB);
+        if (has_partial && t == tp) qv[j] &= pmask;
       } else {
-        qf[nb][t] = ld16(rq, rowoff + (uint32_t)(k0 * 2));
+        qv[j] = ld16(rq, rowoff + (uint32_t)(k0 * 2));
       }
     }
-    qsum[nb] = 0.f;
-    if constexpr (U8) {
-      qsum[nb] = query_row_sum<KS>(qf[nb]);
-    }
   }
+  u32x4_t qf[NQB][KS];
+  float qsum[NQB];
+  auto q_exchange = [&]() {
+#pragma unroll
+    for (int j = 0; j < FPW; ++j) {
+      const int f = wave + NW * j;
+      if (f < NF) qs[f][lane] = qv[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int nb = 0; nb < NQB; ++nb) {
+#pragma unroll
+      for (int t = 0; t < KS; ++t) qf[nb][t] = qs[nb * KS + t][lane];
+      qsum[nb] = 0.f;
+      if constexpr (U8) {
+        qsum[nb] = query_row_sum<KS>(qf[nb]);
+      }
+    }
+  };
 
   // ---- doc stream ----
   const DocRes dr0 = make_doc_res<KIND, VEC>(a, drow, len0);
@@ -124,10 +147,10 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
   }
   // Sequence position -> (doc, tile of that doc); uniform over the wave.
   // Positions past the sequence read an empty range (zeros, no memory access).
-  constexpr bool FIXED = U8;  // fixed load pattern (below)
+  constexpr bool FIXED = U8;  // fixed refill pattern (below)
   const rsrc_t nul = make_rsrc(a.D, 0u);
   auto seq_load = [&](Tile<KIND, KS>& T, int sq) {
-    const bool past = FIXED && sq >= ntiles;
+    const bool past = sq >= ntiles;
     const bool in1 = DOCS == 2 && sq >= nt0;
     // Selects over values: a conditional over the DocRes structs themselves
     // selects their addresses and moves them to scratch memory.
@@ -235,6 +258,12 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
   using RefillAny = std::integral_constant<int, REFILL_ANY>;
 
   Tile<KIND, KS> buf[P];
+  // The first P tiles are loaded unconditionally (past the wave's sequence:
+  // the empty range), so the wait before the query exchange counts exactly
+  // the tile loads issued after the query loads and waits for the query alone.
+#pragma unroll
+  for (int s = 0; s < P; ++s) seq_load(buf[s], wave + NW * s);
+  q_exchange();
   if constexpr (FIXED) {
     // A fixed load pattern: every group of P tiles that has a next group
     // refills all P slots, so the compiler's wait before each tile counts the
@@ -242,8 +271,6 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
     // for all of them). The empty-range loads past the end cost issue slots;
     // fp16/bf16 waves (4-5 tiles each at config 1) lose more to those than
     // they gain, uint8 waves (two docs, ~16 tiles) gain.
-#pragma unroll
-    for (int s = 0; s < P; ++s) seq_load(buf[s], wave + NW * s);
     int i0 = 0;
     for (; i0 + P < my_n; i0 += P) {
 #pragma unroll
@@ -253,9 +280,6 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
     for (int s = 0; s < P; ++s)
       if (i0 + s < my_n) process(RefillNone{}, buf[s], i0 + s);
   } else {
-#pragma unroll
-    for (int s = 0; s < P; ++s)
-      if (s < my_n) seq_load(buf[s], wave + NW * s);
     for (int i0 = 0; i0 < my_n; i0 += P) {
 #pragma unroll
       for (int s = 0; s < P; ++s)
