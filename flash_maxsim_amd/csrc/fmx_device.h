@@ -58,8 +58,16 @@ __device__ __forceinline__ u32x4_t ld16(rsrc_t r, uint32_t voff) {
 __device__ __forceinline__ u32x2_t ld8(rsrc_t r, uint32_t voff) {
   return __builtin_amdgcn_raw_buffer_load_b64(r, voff, 0, 0);
 }
+__device__ __forceinline__ uint32_t ld4(rsrc_t r, uint32_t voff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0);
+}
 __device__ __forceinline__ uint16_t ld2(rsrc_t r, uint32_t voff) {
   return __builtin_amdgcn_raw_buffer_load_b16(r, voff, 0, 0);
+}
+
+// v of lane `src` (0..63), per lane (ds_bpermute: the LDS crossbar, no LDS memory).
+__device__ __forceinline__ uint32_t lane_fetch(uint32_t v, int src) {
+  return (uint32_t)__builtin_amdgcn_ds_bpermute(src * 4, (int)v);
 }
 
 // 16x16x32 MFMA, fp32 accumulate. Operands travel as raw 128-bit registers.

@@ -148,6 +148,8 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
   // Sequence position -> (doc, tile of that doc); uniform over the wave.
   // Positions past the sequence read an empty range (zeros, no memory access).
   constexpr bool FIXED = U8;  // fixed refill pattern (below)
+  constexpr bool GSM = FIXED && VEC;  // group scale loads (below)
+  static_assert(!GSM || P == 4, "group scale loads map 16 lanes per tile slot");
   const rsrc_t nul = make_rsrc(a.D, 0u);
   auto seq_load = [&](Tile<KIND, KS>& T, int sq) {
     const bool past = sq >= ntiles;
@@ -160,7 +162,32 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
     r.s = past ? nul : (in1 ? s1 : s0);
     r.m = past ? nul : (in1 ? n1 : n0);
     r.rowb = dr0.rowb;
-    load_tile<KIND, KS, VEC>(T, r, past ? 0 : (in1 ? sq - nt0 : sq), c, g, koff);
+    load_tile<KIND, KS, VEC, !GSM>(T, r, past ? 0 : (in1 ? sq - nt0 : sq), c, g, koff);
+  };
+  // GSM: the scales and mins of a group of P = 4 tiles come with one dword
+  // load per array (per doc of the workgroup) instead of two 8-byte loads per
+  // tile: lane l loads dword l % 8 of tile slot l / 16 (tokens 2(l % 8) and
+  // 2(l % 8) + 1), and each tile's lanes fetch the two dwords of their four
+  // rows from those lanes. The stream issues a quarter fewer load
+  // instructions, which is what bounds it.
+  auto group_sm = [&](int ig, uint32_t& gs, uint32_t& gm) {
+    const int sq = wave + NW * (ig + (lane >> 4));
+    const bool past = sq >= ntiles;
+    const bool in1 = DOCS == 2 && sq >= nt0;
+    const uint32_t off = (uint32_t)((in1 ? sq - nt0 : sq) * 32 + (lane & 7) * 4);
+    if constexpr (DOCS == 2) {
+      const uint32_t o0 = (past || in1) ? kOOB : off, o1 = (!past && in1) ? off : kOOB;
+      gs = ld4(dr0.s, o0) | ld4(dr1.s, o1);  // out-of-range lanes read zeros
+      gm = ld4(dr0.m, o0) | ld4(dr1.m, o1);
+    } else {
+      gs = ld4(dr0.s, past ? kOOB : off);
+      gm = ld4(dr0.m, past ? kOOB : off);
+    }
+  };
+  auto tile_sm = [&](Tile<KIND, KS>& T, uint32_t gs, uint32_t gm, int slot) {
+    const int src = 16 * slot + 2 * g;  // dwords 2g, 2g+1: tokens 4g .. 4g+3
+    T.s = u32x2_t{lane_fetch(gs, src), lane_fetch(gs, src + 1)};
+    T.m = u32x2_t{lane_fetch(gm, src), lane_fetch(gm, src + 1)};
   };
 
   float m[NQB], m0[NQB];  // running max; m0 holds doc 0's once a wave reaches doc 1
@@ -261,6 +288,8 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
   // The first P tiles are loaded unconditionally (past the wave's sequence:
   // the empty range), so the wait before the query exchange counts exactly
   // the tile loads issued after the query loads and waits for the query alone.
+  uint32_t gsc = 0, gmc = 0, gsn = 0, gmn = 0;  // group scales / mins: current, next
+  if constexpr (GSM) group_sm(0, gsc, gmc);
 #pragma unroll
   for (int s = 0; s < P; ++s) seq_load(buf[s], wave + NW * s);
   q_exchange();
@@ -273,12 +302,22 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
     // they gain, uint8 waves (two docs, ~16 tiles) gain.
     int i0 = 0;
     for (; i0 + P < my_n; i0 += P) {
+      if constexpr (GSM) group_sm(i0 + P, gsn, gmn);
 #pragma unroll
-      for (int s = 0; s < P; ++s) process(RefillAny{}, buf[s], i0 + s);
+      for (int s = 0; s < P; ++s) {
+        if constexpr (GSM) tile_sm(buf[s], gsc, gmc, s);
+        process(RefillAny{}, buf[s], i0 + s);
+      }
+      gsc = gsn;
+      gmc = gmn;
     }
 #pragma unroll
-    for (int s = 0; s < P; ++s)
-      if (i0 + s < my_n) process(RefillNone{}, buf[s], i0 + s);
+    for (int s = 0; s < P; ++s) {
+      if (i0 + s < my_n) {
+        if constexpr (GSM) tile_sm(buf[s], gsc, gmc, s);
+        process(RefillNone{}, buf[s], i0 + s);
+      }
+    }
   } else {
     for (int i0 = 0; i0 < my_n; i0 += P) {
 #pragma unroll

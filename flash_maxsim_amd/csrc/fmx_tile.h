@@ -93,7 +93,8 @@ __device__ __forceinline__ DocRes make_doc_res(const FwdArgs& a, int64_t drow, i
   return r;
 }
 
-template <int KIND, int KS, bool VEC>
+// SM (uint8): also load the tile's scales and mins (else the caller fills T.s, T.m).
+template <int KIND, int KS, bool VEC, bool SM = true>
 __device__ __forceinline__ void load_tile(Tile<KIND, KS>& T, const DocRes& r, int tile, int c, int g,
                                           const uint32_t (&koff)[KS]) {
   const uint32_t base = (uint32_t)(tile * 16 + c) * r.rowb;
@@ -112,7 +113,7 @@ __device__ __forceinline__ void load_tile(Tile<KIND, KS>& T, const DocRes& r, in
 #pragma unroll
     for (int t = 0; t < KS; ++t) T.v[t] = ld16(r.d, base + koff[t]);
   }
-  if constexpr (KIND == KIND_U8) {
+  if constexpr (KIND == KIND_U8 && SM) {
     const uint32_t o = (uint32_t)(tile * 16 + 4 * g) * 2u;
     if constexpr (VEC) {
       T.s = ld8(r.s, o);
