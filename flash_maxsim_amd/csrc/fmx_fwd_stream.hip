@@ -43,7 +43,10 @@ constexpr int stream_depth() { return 4; }
 // 2x and 2x+1 as one tile sequence (the first doc's tiles, then the second's),
 // so its query tile, row sums and load ring carry over from one doc to the
 // next instead of being rebuilt and refilled per doc.
-template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX, bool VEC, int DOCS = 1>
+// JOINT (two padded uint8 docs with aligned rows): the pair's scale rows are
+// adjacent, so one buffer range covers both and the group scale loads (below)
+// take one instruction per array instead of one per doc.
+template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX, bool VEC, int DOCS = 1, bool JOINT = false>
 __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
   constexpr int NW = kStreamWaves, P = stream_depth<KIND>(), QROWS = NQB * 16;
   constexpr int ESZ = KindInfo<KIND>::esz;
@@ -150,6 +153,7 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
   constexpr bool FIXED = U8;  // fixed refill pattern (below)
   constexpr bool GSM = FIXED && VEC;  // group scale loads (below)
   static_assert(!GSM || P == 4, "group scale loads map 16 lanes per tile slot");
+  static_assert(!JOINT || (GSM && DOCS == 2), "a joint scale range serves two-doc group loads");
   const rsrc_t nul = make_rsrc(a.D, 0u);
   auto seq_load = [&](Tile<KIND, KS>& T, int sq) {
     const bool past = sq >= ntiles;
@@ -170,12 +174,23 @@ __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
   // 2(l % 8) + 1), and each tile's lanes fetch the two dwords of their four
   // rows from those lanes. The stream issues a quarter fewer load
   // instructions, which is what bounds it.
+  rsrc_t rsj = nul, rmj = nul;  // JOINT: scale / min rows of both docs
+  if constexpr (JOINT) {
+    const int64_t span = two ? a.sm_b + ((len1 + 3) & ~3) : ((len0 + 3) & ~3);
+    rsj = make_rsrc(a.scales + drow * a.sm_b, (uint32_t)(span * 2));
+    rmj = make_rsrc(a.mins + drow * a.sm_b, (uint32_t)(span * 2));
+  }
   auto group_sm = [&](int ig, uint32_t& gs, uint32_t& gm) {
     const int sq = wave + NW * (ig + (lane >> 4));
     const bool past = sq >= ntiles;
     const bool in1 = DOCS == 2 && sq >= nt0;
     const uint32_t off = (uint32_t)((in1 ? sq - nt0 : sq) * 32 + (lane & 7) * 4);
-    if constexpr (DOCS == 2) {
+    if constexpr (JOINT) {
+      // doc 1's rows start sm_b tokens after doc 0's
+      const uint32_t o = past ? kOOB : (in1 ? (uint32_t)(a.sm_b * 2) + off : off);
+      gs = ld4(rsj, o);
+      gm = ld4(rmj, o);
+    } else if constexpr (DOCS == 2) {
       const uint32_t o0 = (past || in1) ? kOOB : off, o1 = (!past && in1) ? off : kOOB;
       gs = ld4(dr0.s, o0) | ld4(dr1.s, o1);  // out-of-range lanes read zeros
       gm = ld4(dr0.m, o0) | ld4(dr1.m, o1);
@@ -402,8 +417,13 @@ hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
   if constexpr (KIND == KIND_U8 && !ARGMAX) {
     // uint8 docs of one query in one pass: two docs per workgroup.
     if (a.Nq == 1 && npass == 1 && !a.qidx) {
-      hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2>),
-                         dim3((unsigned)((a.B + 1) / 2)), dim3(256), 0, s, a);
+      const dim3 grid((unsigned)((a.B + 1) / 2));
+      // Padded docs whose pair of scale rows stays within the 2^31-byte range.
+      if (VEC && !a.tok_group && (a.sm_b + a.Ld) * 2 + 64 < ((int64_t)1 << 31)) {
+        hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2, VEC>), grid, dim3(256), 0, s, a);
+      } else {
+        hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2>), grid, dim3(256), 0, s, a);
+      }
       return hipGetLastError();
     }
   }
