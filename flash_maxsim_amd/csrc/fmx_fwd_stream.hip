@@ -33,9 +33,11 @@ namespace {
 constexpr int kStreamWaves = 4;
 // Tiles in flight per wave. Deeper uint8 rings (half the bytes per tile) cost
 // the third wave per SIMD, which hides more of the per-tile dequant work than
-// the extra bytes in flight gain.
-template <int KIND>
-constexpr int stream_depth() { return 4; }
+// the extra bytes in flight gain. fp16/bf16 tiles of 8 k-steps (d > 128) hold
+// 8 KB each: two in flight keep two or more waves per SIMD (four cost d = 192
+// and d = 256 with 64-token queries a quarter of their speed, at one wave).
+template <int KIND, int KS>
+constexpr int stream_depth() { return (KIND != KIND_U8 && KS >= 8) ? 2 : 4; }
 
 // KMASK: d is not exactly 32*KS, so fragment slots past d must read as zero.
 // VEC: uint8 vector load path (FwdArgs::vec); true for fp16/bf16.
@@ -48,7 +50,7 @@ constexpr int stream_depth() { return 4; }
 // take one instruction per array instead of one per doc.
 template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX, bool VEC, int DOCS = 1, bool JOINT = false>
 __global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
-  constexpr int NW = kStreamWaves, P = stream_depth<KIND>(), QROWS = NQB * 16;
+  constexpr int NW = kStreamWaves, P = stream_depth<KIND, KS>(), QROWS = NQB * 16;
   constexpr int ESZ = KindInfo<KIND>::esz;
   constexpr bool BF = KindInfo<KIND>::bf;
   constexpr bool U8 = KIND == KIND_U8;
