@@ -530,6 +530,9 @@ hipError_t dispatch(const FwdArgs& a, const TiledPlan& p, bool am, hipStream_t s
       case 6: return dispatch_flags<KIND, kTiledNW, 6, 4>(a, p, am, s);
       case 5: return dispatch_flags<KIND, kTiledNW, 5, 4>(a, p, am, s);
       case 4: return dispatch_flags<KIND, kTiledNW, 4, 4>(a, p, am, s);
+      case 3: return dispatch_flags<KIND, kTiledNW, 3, 4>(a, p, am, s);
+      case 2: return dispatch_flags<KIND, kTiledNW, 2, 4>(a, p, am, s);
+      case 1: return dispatch_flags<KIND, kTiledNW, 1, 4>(a, p, am, s);
       default: break;
     }
   } else if (p.ks == 8) {
@@ -537,6 +540,7 @@ hipError_t dispatch(const FwdArgs& a, const TiledPlan& p, bool am, hipStream_t s
       case 4: return dispatch_flags<KIND, kTiledNW, 4, 8>(a, p, am, s);
       case 3: return dispatch_flags<KIND, kTiledNW, 3, 8>(a, p, am, s);
       case 2: return dispatch_flags<KIND, kTiledNW, 2, 8>(a, p, am, s);
+      case 1: return dispatch_flags<KIND, kTiledNW, 1, 8>(a, p, am, s);
       default: break;
     }
   }
@@ -545,14 +549,26 @@ hipError_t dispatch(const FwdArgs& a, const TiledPlan& p, bool am, hipStream_t s
 
 }  // namespace
 
-bool tiled_fwd_applicable(int64_t Nq, int64_t Lq, int d) { return d >= 1 && d <= 256 && Nq * Lq >= 256; }
+// Batched queries over shared docs read each doc once here instead of once per
+// query (Nq = 2, Lq = 32: 93 against 103 us; Nq = 4: 96 against 198 us at
+// B = 5000, Ld = 300); a single query comes here once it needs more than one
+// pass of the streaming kernel (Lq = 200: 108 against 164 us), below that
+// the streaming kernel is faster (Lq = 96: 82 against 93 us).
+bool tiled_fwd_applicable(int64_t Nq, int64_t Lq, int d) {
+  if (d < 1 || d > 256) return false;
+  return Nq > 1 || Lq > 16 * stream_fwd_nqb(1 << 20, d);
+}
 
 // Picks rows per wave (NB) and doc groups (G). `slots` workgroups run at once
-// (kTiledWPC per CU, two waves per SIMD). The slowest workgroup's MFMA time is
-// proportional to docs-per-group x rows-per-block, so NB is chosen to cut the
-// flattened query rows into nearly full row blocks (3200 rows of config 3:
-// five blocks of 640, where 512-row blocks leave a quarter-full seventh and
-// idle CUs). The XCD-aware mapping puts all row blocks of a doc group on one
+// (kTiledWPC per CU, two waves per SIMD). The slowest workgroup's time is
+// about docs-per-group x (rows-per-block + R0): MFMA work per row plus a
+// per-doc streaming cost worth R0 = 545 rows (fitted: 256 query rows over
+// 5000 docs of 300 tokens take 118, 152, 195 and 231 us with 256-, 512-, 768-
+// and 1024-row blocks). NB is thus chosen to cut the flattened query rows into
+// nearly full row blocks (3200 rows of config 3: five blocks of 640, where
+// 512-row blocks leave a quarter-full seventh and idle CUs), but no smaller
+// than the streaming cost makes worthwhile (512 rows: one 512-row block, not
+// two of 256). The XCD-aware mapping puts all row blocks of a doc group on one
 // XCD (G a multiple of 8, nRB * G / 8 workgroups per XCD), so each doc tile is
 // fetched once per XCD L2; without it the row blocks of a doc meet in the
 // shared last-level cache instead, which is counted as a few percent of extra
@@ -560,14 +576,16 @@ bool tiled_fwd_applicable(int64_t Nq, int64_t Lq, int d) { return d >= 1 && d <=
 TiledPlan tiled_fwd_plan(int64_t Nq, int64_t B, int64_t Lq, int d, int cus) {
   TiledPlan best = {};
   const int ks = d <= 128 ? 4 : 8;
-  const int nbs4[4] = {8, 6, 5, 4}, nbs8[4] = {4, 3, 2, 2};
+  constexpr int kNB = 7;
+  const int nbs4[kNB] = {8, 6, 5, 4, 3, 2, 1}, nbs8[kNB] = {4, 3, 2, 1, 1, 1, 1};
   const int* nbs = ks == 4 ? nbs4 : nbs8;
+  constexpr double kR0 = 545.0;
   const int slots = (cus > 0 ? cus : 256) * kTiledWPC;
   const int per_xcd = slots / 8;
   const int64_t rows = Nq * Lq;
   double best_cost = 0;
   bool have = false;
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kNB; ++i) {
     for (int xcd = 1; xcd >= 0; --xcd) {
       TiledPlan p = {};
       p.ks = ks;
@@ -589,7 +607,8 @@ TiledPlan tiled_fwd_plan(int64_t Nq, int64_t B, int64_t Lq, int d, int cus) {
       p.xcd_map = xcd;
       p.G = G;
       const double rounds = (double)(((int64_t)p.grid + slots - 1) / slots);
-      const double cost = (double)((B + G - 1) / G) * (double)p.rows_per_block * rounds * (xcd ? 1.0 : 1.04);
+      const double cost =
+          (double)((B + G - 1) / G) * ((double)p.rows_per_block + kR0) * rounds * (xcd ? 1.0 : 1.04);
       if (!have || cost < best_cost) {
         best = p;
         best_cost = cost;

@@ -398,6 +398,11 @@ def test_tiled_shapes(oracle_mod, Nq, Lq, B, Ld, d):
     (100, 32, 300, 40, 128),    # 3200 rows: five 640-row blocks (NB = 5)
     (24, 32, 300, 50, 128),     # 768 rows: one 768-row block (NB = 6)
     (12, 32, 300, 64, 256),     # d = 256, 384 rows (NB = 3)
+    (1, 300, 300, 70, 128),     # single query, 300 rows: one 384-row block (NB = 3)
+    (8, 32, 300, 50, 128),      # 256 rows (NB = 2)
+    (3, 64, 300, 45, 96),       # 192 rows, masked width (NB = 2)
+    (2, 32, 300, 60, 128),      # two queries: one 128-row block (NB = 1)
+    (1, 96, 300, 40, 256),      # d = 256, single query past one streaming pass (NB = 1)
 ])
 def test_tiled_row_block_sizes(oracle_mod, Nq, Lq, B, Ld, d):
     # Shapes whose plan (256 CUs) picks each row-block size; the oracle checks

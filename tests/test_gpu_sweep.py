@@ -1,9 +1,11 @@
 """Seeded sweep over the forward kernels' shape classes against the CPU oracle.
 
 Each case draws its own shape from a fixed seed list so the sweep is
-deterministic. It covers the kernel selection boundaries: streaming (few query
-rows), tiled (at least 256 query rows, including DMA-staged exact-width rows
-and VGPR-staged masked widths), split-d (d > 256), single and batched queries,
+deterministic. It covers the kernel selection boundaries: streaming (a single
+query within one pass, per-query docs), tiled (batched queries over shared
+docs, single queries past one streaming pass; row blocks of 128 to 1024 rows,
+DMA-staged exact-width rows and VGPR-staged masked widths), split-d (d > 256),
+single and batched queries,
 shared and per-query docs, ragged lengths (0, 1, Ld, > Ld), fp16 and bf16,
 and uint8 docs in one- and two-doc workgroups. Scores within 1e-2 of the
 float64 oracle on the same input values.
@@ -37,6 +39,10 @@ CASES = [
     (1, 64, 8, 100, 512, torch.float16, True),      # split-d
     (4, 20, 6, 33, 768, torch.bfloat16, True),      # split-d batched, bf16
     (1, 130, 5, 64, 1024, torch.float16, True),     # split-d, two passes
+    (1, 200, 14, 100, 128, torch.float16, True),    # tiled single query, 256-row block
+    (2, 17, 11, 70, 64, torch.bfloat16, True),      # tiled, two short queries, 128-row block
+    (3, 50, 9, 80, 192, torch.float16, True),       # tiled d = 192 (masked), 256-row block
+    (4, 8, 10, 33, 128, torch.float16, True),       # tiled, four 8-token queries
 ]
 
 
