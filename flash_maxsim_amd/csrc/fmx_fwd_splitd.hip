@@ -44,14 +44,31 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, g = lane >> 4;
-  const int pass = blockIdx.y;
+  // Workgroups go to the eight XCDs round-robin. All U units (query, pass) of
+  // one doc share an XCD and start back to back, so the doc streams from HBM
+  // once and the other units read it from that XCD's L2: workgroup
+  // x = 8 * (U * grp + u) + k runs unit u of doc slot 8 * grp + k, where a doc
+  // slot is a shared doc (U = Nq * passes) or a (query, doc) pair (U = passes).
+  const int npass = (a.Lq + QROWS - 1) / QROWS;
+  const bool shared_q = a.shared_docs && a.Nq > 1;
+  const int U = (shared_q ? a.Nq : 1) * npass;
+  const int nslots = shared_q ? a.B : a.Nq * a.B;
+  int slot = blockIdx.x, u = 0;
+  if (U > 1) {
+    const int x = blockIdx.x, k = x & 7, r = x >> 3;
+    const int grp = r / U;
+    u = r - grp * U;
+    slot = 8 * grp + k;
+    if (slot >= nslots) return;  // uniform over the workgroup, before any barrier
+  }
+  const int pass = u % npass;
   int qi, b;
-  if (a.shared_docs && a.Nq > 1) {
-    b = blockIdx.x / a.Nq;
-    qi = blockIdx.x - b * a.Nq;
+  if (shared_q) {
+    b = slot;
+    qi = u / npass;
   } else {
-    qi = blockIdx.x / a.B;
-    b = blockIdx.x - qi * a.B;
+    qi = slot / a.B;
+    b = slot - qi * a.B;
   }
   const int item = qi * a.B + b;
   const int64_t drow = a.shared_docs ? (int64_t)b : (int64_t)item;
@@ -257,10 +274,10 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
     }
     const float total = wave_sum(partsum);
     if (lane == 0) {
-      if (gridDim.y == 1) {
+      if (npass == 1) {
         a.scores[(int64_t)qi * a.ss_n + (int64_t)b * a.ss_b] = total;
       } else {
-        a.partial[(int64_t)pass * gridDim.x + item] = total;  // gridDim.x == Nq*B
+        a.partial[(int64_t)pass * a.Nq * a.B + item] = total;
       }
     }
   }
@@ -281,8 +298,11 @@ hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
   constexpr int QROWS = NQB * 16;
   const int npass = (a.Lq + QROWS - 1) / QROWS;
   const int64_t items = (int64_t)a.Nq * a.B;
-  hipLaunchKernelGGL((splitd_fwd_kernel<KIND, NQB, KSW, KMASK, ARGMAX, VEC>), dim3((unsigned)items, npass),
-                     dim3(512), 0, s, a);
+  const int64_t U = (a.shared_docs && a.Nq > 1 ? a.Nq : 1) * (int64_t)npass;
+  const int64_t nslots = a.shared_docs && a.Nq > 1 ? a.B : items;
+  const int64_t grid = U > 1 ? ((nslots + 7) / 8) * 8 * U : items;
+  hipLaunchKernelGGL((splitd_fwd_kernel<KIND, NQB, KSW, KMASK, ARGMAX, VEC>), dim3((unsigned)grid), dim3(512), 0, s,
+                     a);
   if (npass > 1) {
     hipLaunchKernelGGL(splitd_sum_passes_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, a,
                        npass);
