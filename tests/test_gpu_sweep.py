@@ -43,6 +43,8 @@ CASES = [
     (2, 17, 11, 70, 64, torch.bfloat16, True),      # tiled, two short queries, 128-row block
     (3, 50, 9, 80, 192, torch.float16, True),       # tiled d = 192 (masked), 256-row block
     (4, 8, 10, 33, 128, torch.float16, True),       # tiled, four 8-token queries
+    (2, 150, 7, 60, 128, torch.float16, False),     # stream, per-query docs, two passes on one XCD
+    (3, 40, 5, 30, 640, torch.bfloat16, True),      # split-d, three queries of a shared doc on one XCD
 ]
 
 
@@ -80,7 +82,8 @@ def test_forward_sweep(oracle_mod, case):
 
 
 @pytest.mark.parametrize("B, Lq, Ld, d", [(1, 32, 40, 128), (2, 32, 40, 128), (3, 5, 200, 64),
-                                          (13, 32, 96, 128), (6, 48, 33, 256)])
+                                          (13, 32, 96, 128), (6, 48, 33, 256),
+                                          (11, 100, 70, 128)])  # two 64-token passes
 def test_int8_sweep(oracle_mod, B, Lq, Ld, d):
     seed = 9500 + B * 7 + d
     Q = sim((Lq, d), seed)
