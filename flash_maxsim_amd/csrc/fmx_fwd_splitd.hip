@@ -26,7 +26,9 @@ namespace {
 constexpr int kSplitWaves = 8;
 
 // VEC: uint8 vector load path (FwdArgs::vec); true for fp16/bf16.
-template <int KIND, int NQB, int KSW, bool KMASK, bool ARGMAX, bool VEC>
+// PERSIST (one query, one pass, no query gather): a fixed grid of resident
+// workgroups loads the query slice once and walks docs b, b + G, ...
+template <int KIND, int NQB, int KSW, bool KMASK, bool ARGMAX, bool VEC, bool PERSIST = false>
 __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
   constexpr int NW = kSplitWaves, QROWS = NQB * 16;
   // Tiles in flight per wave: 2 when the query slice takes 128 VGPRs, which
@@ -70,11 +72,6 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
     qi = slot / a.B;
     b = slot - qi * a.B;
   }
-  const int item = qi * a.B + b;
-  const int64_t drow = a.shared_docs ? (int64_t)b : (int64_t)item;
-  int len = a.lengths ? a.lengths[drow] : a.Ld;
-  len = len < 0 ? 0 : (len > a.Ld ? a.Ld : len);
-  const int ntiles = (len + 15) >> 4;
   const bool owner = wave < NQB;  // wave w reduces and maxes query block w
 
   const int tbase = wave * KSW;  // first global k-step of this wave (KSW is even)
@@ -116,6 +113,14 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
       for (int w = 0; w < NW; ++w) qsum += qs_part[w][wave * 16 + c];
     }
   }
+
+  for (;;) {
+  const int item = qi * a.B + b;
+  const int64_t drow = a.shared_docs ? (int64_t)b : (int64_t)item;
+  int len = a.lengths ? a.lengths[drow] : a.Ld;
+  // uniform: the loads below take it into scalar buffer resources
+  len = __builtin_amdgcn_readfirstlane(len < 0 ? 0 : (len > a.Ld ? a.Ld : len));
+  const int ntiles = (len + 15) >> 4;
 
   // ---- doc stream ----
   const DocRes dr = make_doc_res<KIND, VEC>(a, drow, len);
@@ -281,6 +286,11 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
       }
     }
   }
+  if (!PERSIST) break;
+  b += gridDim.x;
+  if (b >= a.B) break;
+  __syncthreads();  // red_m / red_i are rewritten for the next doc
+  }
 }
 
 __global__ void __launch_bounds__(256) splitd_sum_passes_kernel(FwdArgs a, int npass) {
@@ -298,6 +308,33 @@ hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
   constexpr int QROWS = NQB * 16;
   const int npass = (a.Lq + QROWS - 1) / QROWS;
   const int64_t items = (int64_t)a.Nq * a.B;
+  // One query in one pass: resident workgroups walk the docs with the query
+  // slice loaded once (config 5: 201 -> 189 us), for query tiles of 64 rows
+  // or more with aligned rows; smaller tiles gain nothing against more
+  // workgroups per CU, and the masked 128-row instances would spill.
+  if constexpr (NQB >= 4 && VEC && !(KMASK && NQB * KSW >= 32)) {
+   if (npass == 1 && a.Nq == 1 && !a.qidx) {
+    // resident workgroups per CU x CUs (cached per device)
+    static int cache[64] = {0};
+    int dev = 0;
+    int n = 0;
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) n = cache[dev];
+    if (n == 0) {
+      int cus = 0, per = 0;
+      if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+              &per, reinterpret_cast<const void*>(splitd_fwd_kernel<KIND, NQB, KSW, KMASK, ARGMAX, VEC, true>), 512,
+              0) != hipSuccess || per <= 0)
+        per = 1;
+      n = cus * per;
+      if (dev >= 0 && dev < 64) cache[dev] = n;
+    }
+    const int64_t grid = a.B < n ? a.B : n;
+    hipLaunchKernelGGL((splitd_fwd_kernel<KIND, NQB, KSW, KMASK, ARGMAX, VEC, true>), dim3((unsigned)grid), dim3(512),
+                       0, s, a);
+    return hipGetLastError();
+   }
+  }
   const int64_t U = (a.shared_docs && a.Nq > 1 ? a.Nq : 1) * (int64_t)npass;
   const int64_t nslots = a.shared_docs && a.Nq > 1 ? a.B : items;
   const int64_t grid = U > 1 ? ((nslots + 7) / 8) * 8 * U : items;

@@ -57,10 +57,20 @@ struct DocRes {
   uint32_t rowb;  // bytes per token row
 };
 
+// tok_group[drow], taken as wave-uniform (drow is): the buffer resources built
+// from it must sit in scalar registers. A kernel that also stores to memory
+// in the same loop gets a vector load here, whose result the compiler would
+// otherwise treat as varying per lane (and wrap every load in a per-lane loop).
+__device__ __forceinline__ int64_t tok_group_of(const FwdArgs& a, int64_t drow) {
+  const int64_t v = a.tok_group[drow];
+  return (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(v >> 32)) << 32) |
+                   (uint32_t)__builtin_amdgcn_readfirstlane((int)v));
+}
+
 // First element of doc row `drow` of the document operand: drow * sd_b, or
 // for packed docs the start of its token group, 4 * tok_group[drow] rows in.
 __device__ __forceinline__ int64_t doc_elem0(const FwdArgs& a, int64_t drow) {
-  return a.tok_group ? 4 * a.tok_group[drow] * a.sd_l : drow * a.sd_b;
+  return a.tok_group ? 4 * tok_group_of(a, drow) * a.sd_l : drow * a.sd_b;
 }
 
 // VEC (uint8 docs; FwdArgs::vec): code rows are 16-byte aligned and
@@ -75,13 +85,13 @@ __device__ __forceinline__ DocRes make_doc_res(const FwdArgs& a, int64_t drow, i
   r.rowb = (uint32_t)(a.sd_l * ESZ);
   int64_t avail = INT64_MAX;  // token rows from the doc's start to the end of D
   if (a.tok_group) {
-    const int64_t t0 = 4 * a.tok_group[drow];
+    const int64_t t0 = 4 * tok_group_of(a, drow);
     avail = t0 < 0 ? 0 : (a.tok_rows > t0 ? a.tok_rows - t0 : 0);
   }
   const int64_t drows = len < avail ? len : avail;
   r.d = make_rsrc((const char*)a.D + (avail > 0 ? doc_elem0(a, drow) * ESZ : 0), (uint32_t)drows * r.rowb);
   if constexpr (KIND == KIND_U8) {
-    const int64_t sm0 = a.tok_group ? (avail > 0 ? 4 * a.tok_group[drow] : 0) : drow * a.sm_b;
+    const int64_t sm0 = a.tok_group ? (avail > 0 ? 4 * tok_group_of(a, drow) : 0) : drow * a.sm_b;
     int64_t n = VEC ? (int64_t)((len + 3) & ~3) : (int64_t)len;
     if (n > avail) n = avail;
     r.s = make_rsrc(a.scales + sm0, (uint32_t)n * 2u);
