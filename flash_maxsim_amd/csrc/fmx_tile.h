@@ -69,8 +69,11 @@ __device__ __forceinline__ int64_t tok_group_of(const FwdArgs& a, int64_t drow) 
 
 // First element of doc row `drow` of the document operand: drow * sd_b, or
 // for packed docs the start of its token group, 4 * tok_group[drow] rows in.
+// UNIFORM reads tok_group through tok_group_of (the doc resources below); the
+// tiled kernel keeps the plain load (the extra lane reads cost it 2 %).
+template <bool UNIFORM = false>
 __device__ __forceinline__ int64_t doc_elem0(const FwdArgs& a, int64_t drow) {
-  return a.tok_group ? 4 * tok_group_of(a, drow) * a.sd_l : drow * a.sd_b;
+  return a.tok_group ? 4 * (UNIFORM ? tok_group_of(a, drow) : a.tok_group[drow]) * a.sd_l : drow * a.sd_b;
 }
 
 // VEC (uint8 docs; FwdArgs::vec): code rows are 16-byte aligned and
@@ -89,7 +92,7 @@ __device__ __forceinline__ DocRes make_doc_res(const FwdArgs& a, int64_t drow, i
     avail = t0 < 0 ? 0 : (a.tok_rows > t0 ? a.tok_rows - t0 : 0);
   }
   const int64_t drows = len < avail ? len : avail;
-  r.d = make_rsrc((const char*)a.D + (avail > 0 ? doc_elem0(a, drow) * ESZ : 0), (uint32_t)drows * r.rowb);
+  r.d = make_rsrc((const char*)a.D + (avail > 0 ? doc_elem0<true>(a, drow) * ESZ : 0), (uint32_t)drows * r.rowb);
   if constexpr (KIND == KIND_U8) {
     const int64_t sm0 = a.tok_group ? (avail > 0 ? 4 * tok_group_of(a, drow) : 0) : drow * a.sm_b;
     int64_t n = VEC ? (int64_t)((len + 3) & ~3) : (int64_t)len;
