@@ -112,6 +112,36 @@ def test_int8_packed_scores(oracle_mod, Lq, d):
     np.testing.assert_array_equal(out.cpu().numpy(), padded.cpu().numpy())
 
 
+def test_int8_packed_groups_in_any_order():
+    # The contract allows token groups anywhere in [0, T): store the docs of a
+    # packed layout in reverse order (with a gap) and expect identical scores.
+    B, Ld, d, Lq = 37, 70, 128, 32
+    Q = sim((Lq, d), 71)
+    x = sim((B, Ld, d), 72, torch.float32)
+    lengths = torch.randint(0, Ld + 1, (B,), generator=torch.Generator().manual_seed(5), dtype=torch.int32)
+    lengths[:2] = torch.tensor([0, Ld], dtype=torch.int32)
+    packed = fm.quantize_int8_packed(x.to(DEV), lengths.to(DEV))
+    want = fm.flash_maxsim_int8_packed(Q.to(DEV), packed)
+    tg = packed.tok_group.cpu()
+    groups = (packed.lengths.cpu().to(torch.int64) + 3) // 4
+    total = int(groups.sum()) + 5  # five spare groups at the front
+    new_tg = torch.empty_like(tg)
+    codes = torch.zeros(4 * total, d, dtype=torch.uint8, device=DEV)
+    scales = torch.zeros(4 * total, dtype=torch.float16, device=DEV)
+    mins = torch.zeros(4 * total, dtype=torch.float16, device=DEV)
+    at = total
+    for b in range(B):  # doc 0 last in memory, doc B-1 first
+        at -= int(groups[b])
+        new_tg[b] = at
+        src, dst, n = 4 * int(tg[b]), 4 * at, 4 * int(groups[b])
+        codes[dst:dst + n] = packed.codes[src:src + n]
+        scales[dst:dst + n] = packed.scales[src:src + n]
+        mins[dst:dst + n] = packed.mins[src:src + n]
+    moved = fm.PackedInt8Docs(codes, scales, mins, new_tg.to(DEV), packed.lengths, packed.max_len)
+    got = fm.flash_maxsim_int8_packed(Q.to(DEV), moved)
+    np.testing.assert_array_equal(got.cpu().numpy(), want.cpu().numpy())
+
+
 @pytest.mark.parametrize("Lq, d, dtype", [(32, 128, torch.float16), (300, 128, torch.float16),
                                           (32, 1024, torch.float16), (20, 96, torch.bfloat16)])
 def test_packed_scores(oracle_mod, Lq, d, dtype):
