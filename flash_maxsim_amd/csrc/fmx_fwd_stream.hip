@@ -48,8 +48,18 @@ constexpr int stream_depth() { return (KIND != KIND_U8 && KS >= 8) ? 2 : 4; }
 // JOINT (two padded uint8 docs with aligned rows): the pair's scale rows are
 // adjacent, so one buffer range covers both and the group scale loads (below)
 // take one instruction per array instead of one per doc.
+// Waves per SIMD asked of the compiler: three for the one-doc uint8 instance
+// of 64 query rows (the passes of longer queries; 188 VGPRs allowed two, and
+// fitting 168 costs one spill: Lq = 128 139 -> 125 us). The two-doc instance
+// would spill 9 registers in its loop at that budget (75 -> 116 us).
+template <int KIND, int NQB, int KS, bool VEC, int DOCS>
+constexpr int stream_min_waves() {
+  return (KIND == KIND_U8 && VEC && NQB == 4 && KS == 4 && DOCS == 1) ? 3 : 1;
+}
+
 template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX, bool VEC, int DOCS = 1, bool JOINT = false>
-__global__ void __launch_bounds__(256) stream_fwd_kernel(FwdArgs a) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(stream_min_waves<KIND, NQB, KS, VEC, DOCS>())))
+stream_fwd_kernel(FwdArgs a) {
   constexpr int NW = kStreamWaves, P = stream_depth<KIND, KS>(), QROWS = NQB * 16;
   constexpr int ESZ = KindInfo<KIND>::esz;
   constexpr bool BF = KindInfo<KIND>::bf;
