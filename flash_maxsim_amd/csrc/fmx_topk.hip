@@ -133,9 +133,13 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* s
     key[e] = kv;
     valid += kv != 0;
   }
-  // keys present in this chunk (0-keys are padding from an earlier level)
+  // keys present in this chunk (0-keys are padding from an earlier level; at
+  // level 0 every index below n is a key, none of them 0, so no count is needed)
   int total;
-  {
+  if (!keys_in) {
+    const int64_t left = n - c0;
+    total = left < (int64_t)kTopkThreads * kTopkE ? (int)left : kTopkThreads * kTopkE;
+  } else {
     int* tot = &bcast[3];
     block_exclusive_scan(valid, wave_tot, tot);
     total = *tot;
