@@ -174,8 +174,9 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
   // own): REFILL_ANY whether or not that tile exists (past the doc it reads
   // zeros), REFILL_IF only if it does, REFILL_NONE not at all.
   enum { REFILL_NONE, REFILL_IF, REFILL_ANY };
-  auto process = [&](auto mode_tag, Tile<KIND, KSW>& T, int tile) __attribute__((always_inline)) {
+  auto process = [&](auto mode_tag, auto sm_tag, Tile<KIND, KSW>& T, int tile) __attribute__((always_inline)) {
     constexpr int MODE = decltype(mode_tag)::value;
+    constexpr bool SM = decltype(sm_tag)::value;  // this wave loads scales / mins
     u32x4_t af[KSW];
 #pragma unroll
     for (int t = 0; t < KSW; ++t) {
@@ -184,8 +185,8 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
         if (has_partial && t == tp) af[t] &= pmask;
       }
     }
-    float sc[4], off[4];
-    if constexpr (U8) {
+    float sc[4] = {0.f, 0.f, 0.f, 0.f}, off[4] = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (U8 && SM) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) tile_affine(T.s, T.m, r, sc[r], off[r]);
     }
@@ -196,9 +197,9 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int t = 0; t < KSW; ++t) acc[nb] = mfma16x16x32<BF>(af[t], qf[nb][t], acc[nb]);
     }
-    if constexpr (MODE == REFILL_ANY) load_tile<KIND, KSW, VEC>(T, dr, tile + P, c, g, koff);
+    if constexpr (MODE == REFILL_ANY) load_tile<KIND, KSW, VEC, SM>(T, dr, tile + P, c, g, koff);
     if constexpr (MODE == REFILL_IF) {
-      if (tile + P < ntiles) load_tile<KIND, KSW, VEC>(T, dr, tile + P, c, g, koff);
+      if (tile + P < ntiles) load_tile<KIND, KSW, VEC, SM>(T, dr, tile + P, c, g, koff);
     }
     // The first half of the query blocks finished first: store them, then
     // reduce the previous tile while the second half runs.
@@ -231,16 +232,31 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
   // so do uint8 rows without 16-byte alignment (one wave per SIMD fewer).
   constexpr bool FIXED = VEC && !(KMASK && NQB * KSW >= 32);
   if constexpr (FIXED) {
+    // uint8 docs: only the owner waves apply the affine epilogue, so only they
+    // load the tiles' scales and mins; the others run a copy of the loop
+    // without those loads (same tiles and barriers).
+    auto run = [&](auto sm_tag) __attribute__((always_inline)) {
+      constexpr bool SM = decltype(sm_tag)::value;
 #pragma unroll
-    for (int s = 0; s < P; ++s) load_tile<KIND, KSW, VEC>(buf[s], dr, s, c, g, koff);
-    int i0 = 0;
-    for (; i0 + P < ntiles; i0 += P) {
+      for (int s = 0; s < P; ++s) load_tile<KIND, KSW, VEC, SM>(buf[s], dr, s, c, g, koff);
+      int i0 = 0;
+      for (; i0 + P < ntiles; i0 += P) {
 #pragma unroll
-      for (int s = 0; s < P; ++s) process(RefillAny{}, buf[s], i0 + s);
+        for (int s = 0; s < P; ++s) process(RefillAny{}, sm_tag, buf[s], i0 + s);
+      }
+#pragma unroll
+      for (int s = 0; s < P; ++s)
+        if (i0 + s < ntiles) process(RefillNone{}, sm_tag, buf[s], i0 + s);
+    };
+    if constexpr (U8) {
+      if (owner) {
+        run(std::true_type{});
+      } else {
+        run(std::false_type{});
+      }
+    } else {
+      run(std::true_type{});
     }
-#pragma unroll
-    for (int s = 0; s < P; ++s)
-      if (i0 + s < ntiles) process(RefillNone{}, buf[s], i0 + s);
   } else {
 #pragma unroll
     for (int s = 0; s < P; ++s)
@@ -248,7 +264,7 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
     for (int i0 = 0; i0 < ntiles; i0 += P) {
 #pragma unroll
       for (int s = 0; s < P; ++s)
-        if (i0 + s < ntiles) process(RefillIf{}, buf[s], i0 + s);
+        if (i0 + s < ntiles) process(RefillIf{}, std::true_type{}, buf[s], i0 + s);
     }
   }
   if (ntiles > 0) reduce_tile(ntiles - 1, psc, poff);
