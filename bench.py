@@ -4,20 +4,33 @@ Default workload (BASELINE metric): single-query MaxSim, Q[32,128] against
 D[5000,300,128] fp16 (reference flash_maxsim(Q, D)), inputs resident in HBM.
 A step is one flash_maxsim call over the whole batch. value = docs/s.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--config c1|c1_1000|c1_topk|c2|c3|c4|c4_packed|quant|c5|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME] [--rotate R] [--no-cpu]
 
-The other configs are the remaining BASELINE configs (c2-c5), config 1 with
-top-100 selection (c1_topk), config 4 over packed docs (c4_packed), the GPU
-quantiser on config 4's docs (quant) and a
-device copy for counter calibration (copy), for measurement runs; the
-driver's line is the default (c1).
+Configs (the driver's line is the default, c1):
+  c1         metric workload, config 1 at B = 5000
+  c1_rot     the same with four distinct copies of D (1.5 GB) used in turn,
+             so no step finds its docs in the 256 MB last-level cache
+  c1_1000    config 1 at B = 1000 (its parity size)
+  c1_topk    config 1 followed by top-100 selection
+  c2         config 2, visual: Q[1024,128] x D[1000,1024,128]
+  c3         config 3, batched: Q[100,32,128] x D[5000,300,128], shared docs
+  c3_pq      batched with per-query docs (shared_docs=False):
+             Q[100,32,128] x D[100,50,300,128]
+  c4         config 4, uint8 docs [5000,1024,128], lengths U[32,1024]
+  c4_packed  config 4's docs in the packed layout
+  c4_lq128   config 4's docs against a 128-token query
+  mid        the reference's published "medium" row: Q[128,128] x D[1000,1024,128]
+  c5         config 5, training forward + backward, Q[128,1024] x D[1000,512,1024]
+  quant      quantize_int8 of config 4's docs (fp16 source) on the GPU
+  copy       a device copy of 384 MB, to calibrate HBM byte counters
+--rotate R (R >= 2) cycles R copies of the doc tensor(s) for any config.
 
 roofline: the dominant kernel's algorithmic bytes (or flops) per launch divided
 by its average launch duration, timed with HIP events recorded on the stream
-the kernel runs on (torch's current stream, which the library launches on).
-cpu_baseline: the CPU oracle (oracle/, float64 accumulation, all host cores)
-timed on the same workload.
+the kernels run on (torch's current stream, which the library launches on).
+cpu_baseline: the reference's CPU path, maxsim_naive in fp32 (plain torch on
+the host, all threads this process may use), on a bounded sample of the same
+workload (same fp16 values widened to fp32), repeated for about 10 s.
 """
 
 from __future__ import annotations
@@ -36,153 +49,213 @@ HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
 METRIC = "MaxSim docs/sec + % HBM/MFMA roofline, Lq=32 Ld=300 d=128 B=5000 fp16"
-CPU_SAMPLE_S = 10.0  # seconds of CPU oracle work behind cpu_baseline
+CPU_SAMPLE_S = 10.0  # seconds of CPU baseline work
 
 
-def sim(shape, seed, dtype):
+def sim(shape, seed, dtype, device="cpu"):
+    """Reference input recipe: N(0,1) rows, L2-normalised per token, cast."""
     import torch
 
     g = torch.Generator().manual_seed(seed)
-    return torch.nn.functional.normalize(torch.randn(*shape, generator=g), dim=-1).to(dtype)
+    x = torch.nn.functional.normalize(torch.randn(*shape, generator=g), dim=-1).to(dtype)
+    return x.to(device)
 
 
-def make_workload(name):
-    """Returns (description dict, step callable, work units per step, roofline spec, oracle sample fn)."""
-    import numpy as np
+def cpu_threads() -> int:
+    """Host threads for the CPU baseline: the process's CPU share (OMP_NUM_THREADS
+    when set, as on the GPU boxes), else the CPUs it may run on."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env)
+    try:
+        return max(1, len(os.sched_getaffinity(0)))
+    except AttributeError:  # pragma: no cover
+        return max(1, os.cpu_count() or 1)
+
+
+class Workload:
+    """One benchmark configuration.
+
+    steps: callables, each one step of the hot path (several = the same work on
+    rotated copies of the inputs); units: work units per step (docs, pairs);
+    roof: {"bound", "amount" (bytes or flops per step), "unit", "kernel"};
+    cpu_fn / cpu_units: the CPU baseline over a sample of `cpu_units` units.
+    """
+
+    def __init__(self, cfg, steps, units, unit, roof, cpu_fn=None, cpu_units=0, cpu_sample=""):
+        self.cfg, self.steps, self.units, self.unit, self.roof = cfg, steps, units, unit, roof
+        self.cpu_fn, self.cpu_units, self.cpu_sample = cpu_fn, cpu_units, cpu_sample
+
+
+def _copies(t, rotate):
+    """rotate distinct device copies of t (the first is t itself)."""
+    return [t] + [t.clone() for _ in range(max(1, rotate) - 1)]
+
+
+def build(name: str, rotate: int) -> Workload:
     import torch
 
     import flash_maxsim_amd as fm
-    import oracle
 
     dev = "cuda"
-    if name in ("c1", "c1_1000"):
-        B = 5000 if name == "c1" else 1000
-        Lq, Ld, d = 32, 300, 128
-        Q = sim((Lq, d), 11, torch.float16)
-        Dh = sim((B, Ld, d), 12, torch.float16)
-        Qd, Dd = Q.to(dev), Dh.to(dev)
-        cfg = {"workload": f"single-query flash_maxsim Q[{Lq},{d}] x D[{B},{Ld},{d}] fp16", "B": B, "Lq": Lq,
-               "Ld": Ld, "d": d}
-        step = lambda: fm.flash_maxsim(Qd, Dd)  # noqa: E731
-        algo_bytes = B * Ld * d * 2 + Lq * d * 2 + B * 4
-        roof = {"bound": "hbm", "amount": algo_bytes, "unit": "GB/s", "kernel": "stream_fwd_kernel"}
-        Qn, Dn = Q.float().numpy(), Dh.float().numpy()
-        oracle_fn = lambda: oracle.maxsim(Qn, Dn)  # noqa: E731
-        return cfg, step, B, roof, oracle_fn, B, "docs/s"
-    if name == "c1_topk":
-        # Config 1 scoring followed by top-100 selection (fused retrieval call).
-        B, Lq, Ld, d, k = 5000, 32, 300, 128, 100
-        Q = sim((Lq, d), 11, torch.float16)
-        Dh = sim((B, Ld, d), 12, torch.float16)
-        Qd, Dd = Q.to(dev), Dh.to(dev)
-        cfg = {"workload": f"flash_maxsim_topk k={k}: Q[{Lq},{d}] x D[{B},{Ld},{d}] fp16", "B": B, "Lq": Lq,
-               "Ld": Ld, "d": d, "k": k}
-        step = lambda: fm.flash_maxsim_topk(Qd, Dd, k)  # noqa: E731
-        algo_bytes = B * Ld * d * 2 + Lq * d * 2 + B * 4 * 2 + k * 12
-        roof = {"bound": "hbm", "amount": algo_bytes, "unit": "GB/s", "kernel": "stream_fwd_kernel + topk"}
-        Qn, Dn = Q.float().numpy(), Dh.float().numpy()
+    f16 = torch.float16
 
-        def oracle_fn():
-            oracle.topk(oracle.maxsim(Qn, Dn)[0], k)
-
-        return cfg, step, B, roof, oracle_fn, B, "docs/s"
-    if name == "c2":
-        B, Lq, Ld, d = 1000, 1024, 1024, 128
-        Q = sim((Lq, d), 21, torch.float16)
-        Dh = sim((B, Ld, d), 22, torch.float16)
-        Qd, Dd = Q.to(dev), Dh.to(dev)
-        cfg = {"workload": f"single-query flash_maxsim Q[{Lq},{d}] x D[{B},{Ld},{d}] fp16", "B": B, "Lq": Lq,
-               "Ld": Ld, "d": d}
-        step = lambda: fm.flash_maxsim(Qd, Dd)  # noqa: E731
-        roof = {"bound": "mfma", "amount": 2 * Lq * Ld * d * B, "unit": "TFLOP/s", "kernel": "tiled_fwd_kernel"}
-        Qn, Dn = Q.float().numpy(), Dh[:8].float().numpy()
-        oracle_fn = lambda: oracle.maxsim(Qn, Dn)  # noqa: E731
-        return cfg, step, B, roof, oracle_fn, 8, "docs/s"
-    if name == "c3":
-        Nq, B, Lq, Ld, d = 100, 5000, 32, 300, 128
-        Q = sim((Nq, Lq, d), 31, torch.float16)
-        Dh = sim((B, Ld, d), 32, torch.float16)
-        Qd, Dd = Q.to(dev), Dh.to(dev)
-        cfg = {"workload": f"batched flash_maxsim Q[{Nq},{Lq},{d}] x D[{B},{Ld},{d}] fp16 shared docs",
-               "Nq": Nq, "B": B, "Lq": Lq, "Ld": Ld, "d": d}
-        step = lambda: fm.flash_maxsim_batched(Qd, Dd)  # noqa: E731
-        roof = {"bound": "mfma", "amount": 2 * Nq * Lq * Ld * d * B, "unit": "TFLOP/s",
-                "kernel": "tiled_fwd_kernel"}
-        Qn, Dn = Q.float().numpy(), Dh[:50].float().numpy()
-        oracle_fn = lambda: oracle.maxsim(Qn, Dn)  # noqa: E731
-        return cfg, step, Nq * B, roof, oracle_fn, Nq * 50, "pairs/s"
-    if name == "c4":
-        B, Lq, Ld, d = 5000, 32, 1024, 128
-        Q = sim((Lq, d), 41, torch.float16)
-        codes = torch.empty(B, Ld, d, dtype=torch.uint8)
-        scales = torch.empty(B, Ld, 1, dtype=torch.float16)
-        mins = torch.empty(B, Ld, 1, dtype=torch.float16)
-        for b0 in range(0, B, 500):  # bounded host memory
-            Dc = sim((500, Ld, d), 42 + b0, torch.float32)
-            c, s, m = fm.quantize_int8(Dc)
-            codes[b0:b0 + 500], scales[b0:b0 + 500], mins[b0:b0 + 500] = c, s, m
-        lengths = torch.randint(32, 1025, (B,), generator=torch.Generator().manual_seed(43), dtype=torch.int32)
-        Qd, cd, sd, md, ld = (t.to(dev) for t in (Q, codes, scales, mins, lengths))
-        tot = int(lengths.sum())
-        cfg = {"workload": f"int8 fused-dequant varlen flash_maxsim_int8 Q[{Lq},{d}] x D[{B},{Ld},{d}] u8, "
-                           f"len U[32,1024]", "B": B, "Lq": Lq, "Ld": Ld, "d": d, "sum_len": tot}
-        step = lambda: fm.flash_maxsim_int8(Qd, cd, sd, md, ld)  # noqa: E731
-        algo_bytes = tot * (d + 4) + Lq * d * 2 + B * 8
-        roof = {"bound": "hbm", "amount": algo_bytes, "unit": "GB/s", "kernel": "stream_fwd_kernel"}
-        Qn, cn = Q.float().numpy(), codes[:200].numpy()
-        sn, mn, ln = scales[:200].float().numpy(), mins[:200].float().numpy(), lengths[:200].numpy()
-        oracle_fn = lambda: oracle.maxsim_int8(Qn, cn, sn, mn, ln)  # noqa: E731
-        return cfg, step, B, roof, oracle_fn, 200, "docs/s"
-    if name == "c4_packed":
-        # Config 4's docs (same seeds) quantised straight into the packed layout.
-        B, Lq, Ld, d = 5000, 32, 1024, 128
-        Q = sim((Lq, d), 41, torch.float16)
-        lengths = torch.randint(32, 1025, (B,), generator=torch.Generator().manual_seed(43), dtype=torch.int32)
-        Dg = torch.empty(B, Ld, d, dtype=torch.float32, device=dev)
-        for b0 in range(0, B, 500):
-            Dg[b0:b0 + 500] = sim((500, Ld, d), 42 + b0, torch.float32).to(dev)
-        packed = fm.quantize_int8_packed(Dg, lengths)
-        del Dg
+    if name in ("c1", "c1_rot", "c1_1000", "c1_topk"):
+        B = 1000 if name == "c1_1000" else 5000
+        Lq, Ld, d, k = 32, 300, 128, 100
+        if name == "c1_rot":
+            rotate = max(rotate, 4)
+        Q = sim((Lq, d), 11, f16)
+        Dh = sim((B, Ld, d), 12, f16)
         Qd = Q.to(dev)
-        tot = int(lengths.sum())
-        cfg = {"workload": f"int8 packed varlen flash_maxsim_int8_packed Q[{Lq},{d}] x {B} docs of U[32,1024] "
-                           f"tokens, d={d} u8 ({packed.codes.shape[0]} packed rows)", "B": B, "Lq": Lq, "d": d,
-               "sum_len": tot}
-        step = lambda: fm.flash_maxsim_int8_packed(Qd, packed)  # noqa: E731
-        algo_bytes = tot * (d + 4) + Lq * d * 2 + B * 16  # + tok_group, lengths, scores
-        roof = {"bound": "hbm", "amount": algo_bytes, "unit": "GB/s", "kernel": "stream_fwd_kernel"}
-        pc = packed.codes.cpu().numpy()
-        tg, ln = packed.tok_group.cpu().numpy(), lengths.numpy()
-        ps, pm = packed.scales.float().cpu().numpy(), packed.mins.float().cpu().numpy()
-        nb = 200
-        Lmax = int(ln[:nb].max())
-        cn = np.zeros((nb, Lmax, d), np.uint8)
-        sn = np.zeros((nb, Lmax), np.float32)
-        mn = np.zeros((nb, Lmax), np.float32)
-        for b in range(nb):  # padded copies of the first docs for the CPU oracle
-            r0 = 4 * tg[b]
-            cn[b, :ln[b]], sn[b, :ln[b]], mn[b, :ln[b]] = pc[r0:r0 + ln[b]], ps[r0:r0 + ln[b]], pm[r0:r0 + ln[b]]
-        Qn, lnb = Q.float().numpy(), ln[:nb]
-        oracle_fn = lambda: oracle.maxsim_int8(Qn, cn, sn, mn, lnb)  # noqa: E731
-        return cfg, step, B, roof, oracle_fn, nb, "docs/s"
-    if name == "quant":
-        # quantize_int8 of config 4's docs on the GPU (HIP encoder), fp16 source.
+        Ds = _copies(Dh.to(dev), rotate)
+        cfg = {"workload": f"single-query flash_maxsim Q[{Lq},{d}] x D[{B},{Ld},{d}] fp16", "B": B, "Lq": Lq,
+               "Ld": Ld, "d": d}
+        if rotate > 1:
+            cfg["rotated_doc_copies"] = len(Ds)
+        algo = B * Ld * d * 2 + Lq * d * 2 + B * 4
+        Qc, Dc = Q.float(), Dh.float()
+        if name == "c1_topk":
+            cfg["workload"] = f"flash_maxsim_topk k={k}: " + cfg["workload"]
+            cfg["k"] = k
+            steps = [lambda D=D: fm.flash_maxsim_topk(Qd, D, k) for D in Ds]
+            roof = {"bound": "hbm", "amount": algo + B * 4 + k * 12, "unit": "GB/s",
+                    "kernel": "stream_fwd_kernel + topk"}
+            cpu = lambda: torch.topk(fm.maxsim_naive(Qc, Dc), k)  # noqa: E731
+            sample = f"maxsim_naive fp32 + torch.topk over all {B} docs"
+        else:
+            steps = [lambda D=D: fm.flash_maxsim(Qd, D) for D in Ds]
+            roof = {"bound": "hbm", "amount": algo, "unit": "GB/s", "kernel": "stream_fwd_kernel"}
+            cpu = lambda: fm.maxsim_naive(Qc, Dc)  # noqa: E731
+            sample = f"maxsim_naive fp32 over all {B} docs"
+        return Workload(cfg, steps, B, "docs/s", roof, cpu, B, sample)
+
+    if name in ("c2", "mid"):
+        B, Lq, Ld, d = 1000, (1024 if name == "c2" else 128), 1024, 128
+        Q = sim((Lq, d), 21 if name == "c2" else 25, f16)
+        Dh = sim((B, Ld, d), 22 if name == "c2" else 26, f16)
+        Qd = Q.to(dev)
+        Ds = _copies(Dh.to(dev), rotate)
+        cfg = {"workload": f"single-query flash_maxsim Q[{Lq},{d}] x D[{B},{Ld},{d}] fp16", "B": B, "Lq": Lq,
+               "Ld": Ld, "d": d}
+        if rotate > 1:
+            cfg["rotated_doc_copies"] = len(Ds)
+        steps = [lambda D=D: fm.flash_maxsim(Qd, D) for D in Ds]
+        if name == "c2":
+            roof = {"bound": "mfma", "amount": 2 * Lq * Ld * d * B, "unit": "TFLOP/s", "kernel": "tiled_fwd_kernel"}
+        else:
+            roof = {"bound": "hbm", "amount": B * Ld * d * 2 + Lq * d * 2 + B * 4, "unit": "GB/s",
+                    "kernel": "stream_fwd_kernel"}
+        n = 100 if name == "c2" else 500
+        Qc, Dc = Q.float(), Dh[:n].float()
+
+        def cpu():
+            for b0 in range(0, n, 50):  # chunks of 50 docs bound the similarity tensor
+                fm.maxsim_naive(Qc, Dc[b0:b0 + 50])
+
+        return Workload(cfg, steps, B, "docs/s", roof, cpu, n,
+                        f"maxsim_naive fp32 over the first {n} docs in chunks of 50")
+
+    if name in ("c3", "c3_pq"):
+        Nq, Lq, Ld, d = 100, 32, 300, 128
+        B = 5000 if name == "c3" else 50
+        Q = sim((Nq, Lq, d), 31, f16)
+        shape = (B, Ld, d) if name == "c3" else (Nq, B, Ld, d)
+        Dh = sim(shape, 32 if name == "c3" else 33, f16)
+        Qd = Q.to(dev)
+        Ds = _copies(Dh.to(dev), rotate)
+        shared = name == "c3"
+        desc = "shared docs" if shared else "per-query docs (shared_docs=False)"
+        cfg = {"workload": f"batched flash_maxsim Q[{Nq},{Lq},{d}] x D{list(shape)} fp16 {desc}", "Nq": Nq,
+               "B": B, "Lq": Lq, "Ld": Ld, "d": d}
+        if rotate > 1:
+            cfg["rotated_doc_copies"] = len(Ds)
+        steps = [lambda D=D: fm.flash_maxsim_batched(Qd, D, None, shared) for D in Ds]
+        if shared:
+            roof = {"bound": "mfma", "amount": 2 * Nq * Lq * Ld * d * B, "unit": "TFLOP/s",
+                    "kernel": "tiled_fwd_kernel"}
+            n = 500
+            Qc, Dc = Q.float(), Dh[:n].float()
+
+            def cpu():  # per-query loop, as the reference benchmark runs its naive batched case
+                for qi in range(Nq):
+                    fm.maxsim_naive(Qc[qi], Dc)
+
+            return Workload(cfg, steps, Nq * B, "pairs/s", roof, cpu, Nq * n,
+                            f"maxsim_naive fp32, per-query loop over {Nq} queries x the first {n} docs")
+        roof = {"bound": "hbm", "amount": Nq * B * Ld * d * 2 + Nq * Lq * d * 2 + Nq * B * 4, "unit": "GB/s",
+                "kernel": "stream_fwd_kernel"}
+        Qc, Dc = Q.float(), Dh.float()
+
+        def cpu():
+            for qi in range(Nq):
+                fm.maxsim_naive(Qc[qi], Dc[qi])
+
+        return Workload(cfg, steps, Nq * B, "pairs/s", roof, cpu, Nq * B,
+                        f"maxsim_naive fp32, per-query loop over all {Nq} x {B} pairs")
+
+    if name in ("c4", "c4_packed", "c4_lq128"):
         B, Ld, d = 5000, 1024, 128
-        Dg = torch.empty(B, Ld, d, dtype=torch.float16, device=dev)
+        Lq = 128 if name == "c4_lq128" else 32
+        Q = sim((Lq, d), 41 if Lq == 32 else 45, f16)
+        lengths = torch.randint(32, 1025, (B,), generator=torch.Generator().manual_seed(43), dtype=torch.int32)
+        tot = int(lengths.sum())
+        codes = torch.empty(B, Ld, d, dtype=torch.uint8, device=dev)
+        scales = torch.empty(B, Ld, 1, dtype=f16, device=dev)
+        mins = torch.empty(B, Ld, 1, dtype=f16, device=dev)
+        for b0 in range(0, B, 500):  # quantize_int8 on the GPU: bit-identical to the torch formula
+            x = sim((500, Ld, d), 42 + b0, torch.float32, dev)
+            codes[b0:b0 + 500], scales[b0:b0 + 500], mins[b0:b0 + 500] = fm.quantize_int8(x)
+            del x
+        Qd, ld = Q.to(dev), lengths.to(dev)
+        n = 300
+        cc, cs, cm, cl = codes[:n].cpu(), scales[:n].cpu(), mins[:n].cpu(), lengths[:n]
+        Qc = Q.float()
+        cpu = lambda: fm.maxsim_naive(Qc, fm.dequantize_int8(cc, cs, cm), cl)  # noqa: E731
+        sample = f"maxsim_naive fp32 against dequantize_int8 of the first {n} docs, with their lengths"
+        if name == "c4_packed":
+            Dg = torch.empty(B, Ld, d, dtype=torch.float32, device=dev)
+            for b0 in range(0, B, 500):
+                Dg[b0:b0 + 500] = sim((500, Ld, d), 42 + b0, torch.float32, dev)
+            packed = fm.quantize_int8_packed(Dg, lengths)
+            del Dg, codes, scales, mins
+            packs = [packed] + [fm.PackedInt8Docs(packed.codes.clone(), packed.scales.clone(), packed.mins.clone(),
+                                                  packed.tok_group, packed.lengths, packed.max_len)
+                                for _ in range(max(1, rotate) - 1)]
+            cfg = {"workload": f"int8 packed varlen flash_maxsim_int8_packed Q[{Lq},{d}] x {B} docs of "
+                               f"U[32,1024] tokens, d={d} u8 ({packed.codes.shape[0]} packed rows)", "B": B,
+                   "Lq": Lq, "d": d, "sum_len": tot}
+            steps = [lambda p=p: fm.flash_maxsim_int8_packed(Qd, p) for p in packs]
+            algo = tot * (d + 4) + Lq * d * 2 + B * 16  # + tok_group, lengths, scores
+        else:
+            sets = [(codes, scales, mins)] + [(codes.clone(), scales.clone(), mins.clone())
+                                              for _ in range(max(1, rotate) - 1)]
+            cfg = {"workload": f"int8 fused-dequant varlen flash_maxsim_int8 Q[{Lq},{d}] x D[{B},{Ld},{d}] u8, "
+                               f"len U[32,1024]", "B": B, "Lq": Lq, "Ld": Ld, "d": d, "sum_len": tot}
+            steps = [lambda s=s: fm.flash_maxsim_int8(Qd, s[0], s[1], s[2], ld) for s in sets]
+            algo = tot * (d + 4) + Lq * d * 2 + B * 8
+        if rotate > 1:
+            cfg["rotated_doc_copies"] = len(steps)
+        roof = {"bound": "hbm", "amount": algo, "unit": "GB/s", "kernel": "stream_fwd_kernel"}
+        return Workload(cfg, steps, B, "docs/s", roof, cpu, n, sample)
+
+    if name == "quant":
+        B, Ld, d = 5000, 1024, 128
+        Dg = torch.empty(B, Ld, d, dtype=f16, device=dev)
         for b0 in range(0, B, 500):
-            Dg[b0:b0 + 500] = sim((500, Ld, d), 42 + b0, torch.float16).to(dev)
+            Dg[b0:b0 + 500] = sim((500, Ld, d), 42 + b0, f16, dev)
         cfg = {"workload": f"quantize_int8 of D[{B},{Ld},{d}] fp16 -> u8 codes + fp16 scales/mins", "B": B,
                "Ld": Ld, "d": d}
-        step = lambda: fm.quantize_int8(Dg)  # noqa: E731
-        algo_bytes = B * Ld * (d * 2 + d + 4)
-        roof = {"bound": "hbm", "amount": algo_bytes, "unit": "GB/s", "kernel": "quantize_kernel"}
-        Dn = Dg[:20].float().cpu().numpy()
-        oracle_fn = lambda: oracle.quantize_int8(Dn)  # noqa: E731
-        return cfg, step, B, roof, oracle_fn, 20, "docs/s"
+        roof = {"bound": "hbm", "amount": B * Ld * (d * 2 + d + 4), "unit": "GB/s", "kernel": "quantize_kernel"}
+        n = 100
+        Dc = Dg[:n].cpu()
+        return Workload(cfg, [lambda: fm.quantize_int8(Dg)], B, "docs/s", roof, lambda: fm.quantize_int8(Dc), n,
+                        f"quantize_int8 (torch formula) on the CPU over the first {n} docs")
+
     if name == "c5":
         B, Lq, Ld, d = 1000, 128, 512, 1024
-        Q = sim((Lq, d), 51, torch.float16)
-        Dh = sim((B, Ld, d), 52, torch.float16)
+        Q = sim((Lq, d), 51, f16)
+        Dh = sim((B, Ld, d), 52, f16)
         Qd = Q.to(dev).requires_grad_(True)
         Dd = Dh.to(dev).requires_grad_(True)
 
@@ -196,24 +269,28 @@ def make_workload(name):
                "Lq": Lq, "Ld": Ld, "d": d}
         # D read by the forward + dD written + the B*Lq rows of D gathered for dQ
         # + argmax written and read back (Q, dQ and scores are < 1 MB).
-        algo_bytes = 2 * B * Ld * d * 2 + B * Lq * d * 2 + B * Lq * 4 * 2
-        roof = {"bound": "hbm", "amount": algo_bytes, "unit": "GB/s", "kernel": "splitd_fwd_kernel + bwd kernels (whole step)"}
-        Qn, Dn = Q.float().numpy(), Dh[:4].float().numpy()
+        roof = {"bound": "hbm", "amount": 2 * B * Ld * d * 2 + B * Lq * d * 2 + B * Lq * 4 * 2, "unit": "GB/s",
+                "kernel": "splitd_fwd_kernel + bwd kernels (whole step)"}
+        n = 8
+        Qc = Q.float().requires_grad_(True)
+        Dc = Dh[:n].float().requires_grad_(True)
 
-        def oracle_fn():
-            s, am, _ = oracle.maxsim(Qn, Dn, want_argmax=True)
-            oracle.bwd(Qn, Dn, am, np.ones(4))
+        def cpu():  # fp32 autograd through maxsim_naive, as the reference benchmark's naive training
+            fm.maxsim_naive(Qc, Dc).sum().backward()
+            Qc.grad = None
+            Dc.grad = None
 
-        return cfg, step, B, roof, oracle_fn, 4, "docs/s"
+        return Workload(cfg, [step], B, "docs/s", roof, cpu, n,
+                        f"maxsim_naive fp32 forward + autograd backward over the first {n} docs")
+
     if name == "copy":
-        # Calibration for HBM byte counters: a plain device copy of the metric's D size.
         n = 5000 * 300 * 128
-        src = torch.empty(n, dtype=torch.float16, device=dev).normal_()
+        src = torch.empty(n, dtype=f16, device=dev).normal_()
         dst = torch.empty_like(src)
         cfg = {"workload": f"device copy of {n * 2} bytes (counter calibration)", "bytes": n * 2}
-        step = lambda: dst.copy_(src)  # noqa: E731
         roof = {"bound": "hbm", "amount": 2 * n * 2, "unit": "GB/s", "kernel": "copy"}
-        return cfg, step, 1, roof, (lambda: None), 1, "copies/s"
+        return Workload(cfg, [lambda: dst.copy_(src)], 1, "copies/s", roof)
+
     raise SystemExit(f"unknown config {name}")
 
 
@@ -249,8 +326,8 @@ def main():
     # should see the clocks the GPU settles at, not that transient.
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=300)
-    ap.add_argument("--config", default="c1",
-                    help="c1 (metric), c1_1000, c1_topk, c2, c3, c4, c4_packed, quant, c5, copy")
+    ap.add_argument("--config", default="c1", help="workload name (see the module docstring)")
+    ap.add_argument("--rotate", type=int, default=1, help="cycle this many copies of the docs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -258,15 +335,13 @@ def main():
               "multi-GPU path (docs sharded across GPUs) is described in DESIGN.md, not run.", file=sys.stderr)
         raise SystemExit(2)
 
-    import numpy as np
     import torch
 
-    import oracle
-
     torch.cuda.set_device(0)
-    cfg, step, units, roof, oracle_fn, oracle_units, unit = make_workload(args.config)
-    for _ in range(args.warmup):
-        step()
+    w = build(args.config, args.rotate)
+    steps = w.steps
+    for i in range(args.warmup):
+        steps[i % len(steps)]()
     torch.cuda.synchronize()
 
     # The library launches on torch's current stream; one event pair brackets the
@@ -278,15 +353,16 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ev_start.record(stream)
-    for _ in range(args.steps):
-        step()
+    for i in range(args.steps):
+        steps[i % len(steps)]()
     ev_end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1000.0 / args.steps
     kern_ms = ev_start.elapsed_time(ev_end) / args.steps  # average launch duration on the kernel's stream
-    value = units / (ms_per_step / 1000.0)
+    value = w.units / (ms_per_step / 1000.0)
 
+    roof = w.roof
     achieved = roof["amount"] / (kern_ms / 1000.0)
     if roof["unit"] == "GB/s":
         achieved /= 1e9
@@ -301,28 +377,30 @@ def main():
                 "kernel_ms": round(kern_ms, 5)}
 
     cpu = None
-    if not args.no_cpu and args.config != "copy":
-        # Bounded sample: the oracle over `oracle_units` items of the same
-        # workload, repeated until at least CPU_SAMPLE_S seconds have run.
-        threads = oracle.default_threads()
-        oracle_fn()  # warm
-        calls = 0
-        t = time.perf_counter()
-        while True:
-            oracle_fn()
-            calls += 1
-            el = time.perf_counter() - t
-            if el >= CPU_SAMPLE_S and calls >= 3:
-                break
-        cpu = {"value": round(oracle_units * calls / el, 2), "unit": unit, "cores": threads, "kind": "port",
-               "sample": f"{calls} x {oracle_units} {unit.split('/')[0]} of the same workload "
-                         f"({el:.1f} s), float64 oracle (oracle/maxsim_oracle.c) on {threads} threads, "
-                         f"{cpu_model()}"}
+    if not args.no_cpu and w.cpu_fn is not None:
+        # Bounded sample: the reference's CPU path over `cpu_units` units of the
+        # same workload, repeated until at least CPU_SAMPLE_S seconds have run.
+        threads = cpu_threads()
+        torch.set_num_threads(threads)
+        with torch.inference_mode(args.config != "c5"):
+            w.cpu_fn()  # warm
+            calls = 0
+            t = time.perf_counter()
+            while True:
+                w.cpu_fn()
+                calls += 1
+                el = time.perf_counter() - t
+                if el >= CPU_SAMPLE_S and calls >= 3:
+                    break
+        what = w.unit.split("/")[0]
+        cpu = {"value": round(w.cpu_units * calls / el, 2), "unit": w.unit, "cores": threads, "kind": "port",
+               "sample": f"{calls} x {w.cpu_units} {what} ({el:.1f} s): {w.cpu_sample}, "
+                         f"torch {torch.__version__} on {threads} threads, {cpu_model()}"}
 
     line = {
-        "metric": METRIC if args.config == "c1" else f"{args.config}: {cfg['workload']}",
+        "metric": METRIC if args.config == "c1" and args.rotate <= 1 else f"{args.config}: {w.cfg['workload']}",
         "value": round(value, 1),
-        "unit": unit,
+        "unit": w.unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -330,9 +408,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16",
+        "dtype": "f16",  # MFMA operands (uint8 codes are widened to fp16 exactly), fp32 accumulation
         "data": "synthetic",
-        "config": cfg,
+        "config": w.cfg,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

@@ -470,9 +470,10 @@ int fmx_bwd_batched(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stri
   if ((dQ && !aligned16(dQ)) || (dD && !aligned16(dD))) return fail(FMX_ERR_INVALID, "dQ and dD must be 16-byte aligned");
   if (Nq > 1 && (q_stride_n & 7)) return fail(FMX_ERR_INVALID, "Q query stride must be a multiple of 8");
   if (dD) {
-    if (Nq * Lq >= 8192 || Ld >= (1 << 19))
-      return fail(FMX_ERR_UNSUPPORTED, "dD kernel covers Nq*Lq < 8192 and Ld < 2^19 (Nq*Lq=%lld, Ld=%lld)",
-                  (long long)(Nq * Lq), (long long)Ld);
+    if (Ld >= (1 << 19))
+      return fail(FMX_ERR_UNSUPPORTED, "dD needs Ld < 2^19 (Ld=%lld)", (long long)Ld);
+    if (Nq * Lq >= INT32_MAX || fmx::bwd_dd_chunks(Nq * Lq) > 65535)
+      return fail(FMX_ERR_UNSUPPORTED, "Nq*Lq=%lld too large", (long long)(Nq * Lq));
   }
   const size_t dd_ws = dD ? bwd_dd_ws(Nq, B, Lq, Ld) : 0;
   const size_t need = dd_ws + (dQ ? bwd_dq_ws(Nq, B, Lq, d) : 0);
@@ -490,7 +491,8 @@ int fmx_bwd_batched(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stri
   if (workspace) {
     char* w = static_cast<char*>(workspace);
     a.dd_rows = reinterpret_cast<uint32_t*>(w);
-    a.dd_ent = reinterpret_cast<uint16_t*>(w + (size_t)B * (size_t)Ld * sizeof(uint32_t));
+    a.dd_ent = reinterpret_cast<uint16_t*>(w + (size_t)fmx::bwd_dd_chunks(Nq * Lq) * (size_t)B * (size_t)Ld *
+                                           sizeof(uint32_t));
     a.ws = reinterpret_cast<float*>(w + dd_ws);
   }
   a.dd_slab = fmx::bwd_dd_slab((int)d);
@@ -507,6 +509,7 @@ int fmx_bwd_batched(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stri
   a.d = (int)d;
   a.nchunk = fmx::bwd_dq_chunks((int)B, (int)(Nq * Lq), (int)d);
   a.sort_n = fmx::bwd_sort_n(Nq * Lq);
+  a.dd_chunks = (int)fmx::bwd_dd_chunks(Nq * Lq);
   const int kind = dtype == FMX_DTYPE_BF16 ? fmx::KIND_BF16 : fmx::KIND_F16;
   return hip_status(fmx::launch_bwd(kind, a, static_cast<hipStream_t>(stream)), "fmx_bwd launch");
 }

@@ -133,26 +133,32 @@ __global__ void __launch_bounds__(256) bwd_dq_finalize_kernel(BwdArgs a) {
   static_cast<uint16_t*>(a.dQ)[i] = Elem<BF>::from_f(s);
 }
 
-constexpr int kEntryBits = 13;  // (query, token) entries per doc < 2^13
+constexpr int kEntryBits = 13;  // entries of one chunk < 2^13 (kDdChunk)
 constexpr uint32_t kNoRow = 0xffffffffu;
 
-// dD index, one workgroup per doc. The doc's (query, token) entries become
-// keys row << 13 | entry in LDS, bitonic-sorted, so each picked row's entries
-// are contiguous and in entry order. Written to the workspace:
-//   ent[b][p]    entry of sorted position p (uint16), p < Nq*Lq
-//   rows[b][j]   first sorted position | count << 16 of row j, or kNoRow.
-// Docs of length 0 pick no rows.
-__device__ __forceinline__ void dd_index_block(const BwdArgs& a, int b, uint32_t* keys) {
+// dD index, one workgroup per (doc, chunk of kDdChunk consecutive (query,
+// token) entries). The chunk's entries e become keys row << 13 | (e - e0) in
+// LDS, bitonic-sorted, so each picked row's entries are contiguous and in
+// entry order. Written to the workspace:
+//   ent[b][e0 + p]     chunk-local entry of sorted position p (uint16)
+//   rows[c][b][j]      first sorted position | count << 16 of row j within
+//                      chunk c, or kNoRow.
+// Chunks hold consecutive entries, so a row's entries taken chunk by chunk
+// are in entry order. Docs of length 0 pick no rows.
+__device__ __forceinline__ void dd_index_block(const BwdArgs& a, int b, int chunk, uint32_t* keys) {
   const int NL = a.Nq * a.Lq;
+  const int e0 = chunk * kDdChunk;
+  const int n = NL - e0 < kDdChunk ? NL - e0 : kDdChunk;  // entries of this chunk
   const bool empty = a.lengths && doc_len(a, b) == 0;
-  for (int e = threadIdx.x; e < a.sort_n; e += 256) {
+  for (int p = threadIdx.x; p < a.sort_n; p += 256) {
     uint32_t key = kNoRow;
-    if (e < NL && !empty) {
+    if (p < n && !empty) {
+      const int e = e0 + p;
       const int qi = e / a.Lq, q = e - qi * a.Lq;
       const int j = clamp_index(a.argmax[((int64_t)qi * a.B + b) * a.Lq + q], a.Ld);
-      key = ((uint32_t)j << kEntryBits) | (uint32_t)e;
+      key = ((uint32_t)j << kEntryBits) | (uint32_t)p;
     }
-    keys[e] = key;
+    keys[p] = key;
   }
   __syncthreads();
   for (int size = 2; size <= a.sort_n; size <<= 1) {
@@ -170,22 +176,22 @@ __device__ __forceinline__ void dd_index_block(const BwdArgs& a, int b, uint32_t
       __syncthreads();
     }
   }
-  uint16_t* ent = a.dd_ent + (int64_t)b * NL;
-  for (int p = threadIdx.x; p < NL; p += 256) ent[p] = (uint16_t)(keys[p] & ((1u << kEntryBits) - 1));
-  uint32_t* rows = a.dd_rows + (int64_t)b * a.Ld;
+  uint16_t* ent = a.dd_ent + (int64_t)b * NL + e0;
+  for (int p = threadIdx.x; p < n; p += 256) ent[p] = (uint16_t)(keys[p] & ((1u << kEntryBits) - 1));
+  uint32_t* rows = a.dd_rows + ((int64_t)chunk * a.B + b) * a.Ld;
   for (int j = threadIdx.x; j < a.Ld; j += 256) {
     // first sorted position with row >= j (keys of empty slots are kNoRow)
     const uint32_t lo_key = (uint32_t)j << kEntryBits;
-    int lo = 0, hi = NL;
+    int lo = 0, hi = n;
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
       if (keys[mid] < lo_key) lo = mid + 1; else hi = mid;
     }
     uint32_t info = kNoRow;
-    if (lo < NL && (keys[lo] >> kEntryBits) == (uint32_t)j) {
-      int n = 1;
-      while (lo + n < NL && (keys[lo + n] >> kEntryBits) == (uint32_t)j) ++n;
-      info = (uint32_t)lo | ((uint32_t)n << 16);
+    if (lo < n && (keys[lo] >> kEntryBits) == (uint32_t)j) {
+      int cnt = 1;
+      while (lo + cnt < n && (keys[lo + cnt] >> kEntryBits) == (uint32_t)j) ++cnt;
+      info = (uint32_t)lo | ((uint32_t)cnt << 16);
     }
     rows[j] = info;
   }
@@ -218,23 +224,29 @@ __device__ __forceinline__ void dd_write_block(const BwdArgs& a, int slab) {
   const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (; r < r1; r += step) {
     uint16_t* orow = static_cast<uint16_t*>(a.dD) + r * a.d;
-    const uint32_t info = a.dd_rows[r];
-    if (info == kNoRow) {
+    const uint32_t info0 = a.dd_rows[r];
+    if (a.dd_chunks == 1 && info0 == kNoRow) {
       for (int kc = kc0; kc < nkc; kc += 64) store8<BF>(orow, kc * 8, a.d, zero);
     } else {
-      const uint16_t* ent = a.dd_ent + (int64_t)b * NL + (info & 0xffffu);
-      const int n = (int)(info >> 16);
       for (int kc = kc0; kc < nkc; kc += 64) {
         const int k0 = kc * 8;
         float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int i = 0; i < n; ++i) {
-          const int e = ent[i];
-          const int qi = e / a.Lq, q = e - qi * a.Lq;
-          const float g = a.grad[(int64_t)qi * a.g_n + (int64_t)b * a.g_b];
-          float x[8];
-          load8<BF>(Q + (int64_t)qi * a.sq_n + (int64_t)q * a.sq_l, k0, a.d, x);
+        // the row's entries chunk by chunk: entry order overall
+        for (int ch = 0; ch < a.dd_chunks; ++ch) {
+          const uint32_t info = ch == 0 ? info0 : a.dd_rows[(int64_t)ch * total + r];
+          if (info == kNoRow) continue;
+          const int e0 = ch * kDdChunk;
+          const uint16_t* ent = a.dd_ent + (int64_t)b * NL + e0 + (info & 0xffffu);
+          const int n = (int)(info >> 16);
+          for (int i = 0; i < n; ++i) {
+            const int e = e0 + ent[i];
+            const int qi = e / a.Lq, q = e - qi * a.Lq;
+            const float g = a.grad[(int64_t)qi * a.g_n + (int64_t)b * a.g_b];
+            float x[8];
+            load8<BF>(Q + (int64_t)qi * a.sq_n + (int64_t)q * a.sq_l, k0, a.d, x);
 #pragma unroll
-          for (int k = 0; k < 8; ++k) acc[k] = fmaf(g, x[k], acc[k]);
+            for (int k = 0; k < 8; ++k) acc[k] = fmaf(g, x[k], acc[k]);
+          }
         }
         store8<BF>(orow, k0, a.d, acc);
       }
@@ -254,7 +266,7 @@ __global__ void __launch_bounds__(256) bwd_dq_partial_kernel(BwdArgs a) {
 
 __global__ void __launch_bounds__(256) bwd_dd_index_kernel(BwdArgs a) {
   extern __shared__ uint32_t smem[];
-  dd_index_block(a, blockIdx.x, smem);
+  dd_index_block(a, blockIdx.x, blockIdx.y, smem);
 }
 
 template <bool BF>
@@ -276,7 +288,7 @@ hipError_t launch_bwd_t(const BwdArgs& a, hipStream_t s) {
   }
   if (a.dD && a.B > 0) {
     const size_t lds = bwd_dd_lds_bytes((int64_t)a.Nq * a.Lq);
-    hipLaunchKernelGGL(bwd_dd_index_kernel, dim3((unsigned)a.B), dim3(256), lds, s, a);
+    hipLaunchKernelGGL(bwd_dd_index_kernel, dim3((unsigned)a.B, (unsigned)a.dd_chunks), dim3(256), lds, s, a);
     const int64_t slabs = ((int64_t)a.B * a.Ld + a.dd_slab - 1) / a.dd_slab;
     hipLaunchKernelGGL(bwd_dd_write_kernel<BF>, dim3((unsigned)slabs), dim3(256), 0, s, a);
   }
@@ -298,17 +310,20 @@ int bwd_dq_chunks(int B, int rows, int d) {
   return (int)n;
 }
 
+// Sort size of one dD index chunk: a power of two >= the chunk's entries.
 int bwd_sort_n(int64_t entries) {
   int n = 64;
-  while (n < entries) n <<= 1;
+  while (n < entries && n < kDdChunk) n <<= 1;
   return n;
 }
 
+int64_t bwd_dd_chunks(int64_t entries) { return entries > 0 ? (entries + kDdChunk - 1) / kDdChunk : 1; }
+
 size_t bwd_dd_lds_bytes(int64_t entries) { return (size_t)bwd_sort_n(entries) * sizeof(uint32_t); }
 
-// Workspace of the dD index: rows [B, Ld] uint32, then ent [B, entries] uint16.
+// Workspace of the dD index: rows [chunks, B, Ld] uint32, then ent [B, entries] uint16.
 size_t bwd_dd_index_bytes(int64_t B, int64_t entries, int64_t Ld) {
-  const size_t rows = (size_t)B * (size_t)Ld * sizeof(uint32_t);
+  const size_t rows = (size_t)bwd_dd_chunks(entries) * (size_t)B * (size_t)Ld * sizeof(uint32_t);
   return rows + (((size_t)B * (size_t)entries * sizeof(uint16_t) + 255) & ~(size_t)255);
 }
 

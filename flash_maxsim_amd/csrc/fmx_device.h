@@ -220,10 +220,24 @@ __device__ __forceinline__ float max_over_groups(float v) {
   return vmax(lo, hi);
 }
 
-// (value, index) max where ties go to the smaller index: combining per-lane
-// first-occurrence maxima this way yields the global first occurrence.
+// Running (max, first index) over similarities s of increasing index j, with
+// torch.max's NaN rule: a NaN is the max and the first NaN keeps it (once m
+// is NaN nothing replaces it), otherwise only a strictly larger value moves
+// the index. !(s <= m) is true for s > m and for a NaN s.
+__device__ __forceinline__ void argmax_fold(float s, int j, float& m, int& mi) {
+  if (m == m && !(s <= m)) {
+    m = s;
+    mi = j;
+  }
+}
+
+// (value, index) max where ties go to the smaller index and NaN beats every
+// number (two NaNs: the smaller index): combining per-lane first-occurrence
+// maxima this way yields the global first occurrence of torch.max.
 __device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
-  if (ov > v || (ov == v && oi < i)) {
+  const bool vn = v != v, on = ov != ov;
+  const bool take = on ? (!vn || oi < i) : (!vn && (ov > v || (ov == v && oi < i)));
+  if (take) {
     v = ov;
     i = oi;
   }

@@ -1,9 +1,10 @@
-// Split-d MaxSim forward for large embeddings (256 < d <= 2048).
+// Split-d MaxSim forward for large embeddings (256 < d <= 4096).
 //
 // Same contract as _maxsim_fwd_kernel / _maxsim_int8_kernel (reference
 // flash_maxsim/flash_maxsim.py:80-146, flash_maxsim/flash_maxsim_quant.py:40-98)
 // for shapes whose query tile does not fit one wave's registers. The reference
-// covers those with small Triton blocks (d_pad up to 2048, flash_maxsim.py:29-34).
+// covers those with small Triton blocks (flash_maxsim.py:29-34, any d_pad via the
+// fallback of :71), its tests go to d = 2048.
 //
 // One workgroup of eight waves scores one (query, doc) pair for one pass of up
 // to 16*NQB query tokens. Wave w owns the k-steps [w*KSW, (w+1)*KSW), i.e. the
@@ -152,12 +153,7 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
     }
     if constexpr (ARGMAX) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if (S[r] > m) {
-          m = S[r];
-          mi = row0 + r;
-        }
-      }
+      for (int r = 0; r < 4; ++r) argmax_fold(S[r], row0 + r, m, mi);
     } else {
       m = fold_max4(m, S[0], S[1], S[2], S[3]);
     }
@@ -230,7 +226,7 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
   // drain every other tile at P = 2). The largest masked instances keep
   // conditional loads (the fixed pattern's extra registers spill there), and
   // so do uint8 rows without 16-byte alignment (one wave per SIMD fewer).
-  constexpr bool FIXED = VEC && !(KMASK && NQB * KSW >= 32);
+  constexpr bool FIXED = VEC && !(KMASK && (NQB * KSW >= 32 || KSW >= 16));
   if constexpr (FIXED) {
     // uint8 docs: only the owner waves apply the affine epilogue, so only they
     // load the tiles' scales and mins; the others run a copy of the loop
@@ -384,7 +380,9 @@ template <int KIND, int KSW>
 hipError_t dispatch_nqb(const FwdArgs& a, bool am, hipStream_t s) {
   switch (splitd_fwd_nqb(a.Lq, a.d)) {
     case 1: return dispatch_flags<KIND, 1, KSW>(a, am, s);
-    case 2: return dispatch_flags<KIND, 2, KSW>(a, am, s);
+    case 2:
+      if constexpr (KSW <= 8) return dispatch_flags<KIND, 2, KSW>(a, am, s);
+      return hipErrorInvalidValue;
     case 4:
       if constexpr (KSW <= 4) return dispatch_flags<KIND, 4, KSW>(a, am, s);
       return hipErrorInvalidValue;
@@ -400,27 +398,29 @@ hipError_t dispatch_ksw(const FwdArgs& a, bool am, hipStream_t s) {
     case 2: return dispatch_nqb<KIND, 2>(a, am, s);
     case 4: return dispatch_nqb<KIND, 4>(a, am, s);
     case 8: return dispatch_nqb<KIND, 8>(a, am, s);
+    case 16: return dispatch_nqb<KIND, 16>(a, am, s);
     default: return hipErrorInvalidValue;
   }
 }
 
 }  // namespace
 
-bool splitd_fwd_supported(int d) { return d > 256 && d <= 2048; }
+bool splitd_fwd_supported(int d) { return d > 256 && d <= 4096; }
 
 // k-steps per wave: the eight slices of 32*KSW cover d.
 int splitd_fwd_ksw(int d) {
   const int steps = (d + 31) / 32;
   const int ksw = (steps + kSplitWaves - 1) / kSplitWaves;
-  return ksw <= 2 ? 2 : ksw <= 4 ? 4 : 8;
+  return ksw <= 2 ? 2 : ksw <= 4 ? 4 : ksw <= 8 ? 8 : 16;
 }
 
 // Query blocks per pass, capped so the query slice stays within 128 VGPRs
-// (64 at KSW = 8, where the deeper doc fragments need the rest).
+// (64 at KSW >= 8, where the deeper doc fragments need the rest: at KSW = 16
+// one block's slice and two 16-step tiles take 192 of the 256).
 int splitd_fwd_nqb(int Lq, int d) {
   const int need = (Lq + 15) / 16;
   const int ksw = splitd_fwd_ksw(d);
-  const int cap = ksw >= 8 ? 2 : 32 / ksw;
+  const int cap = ksw >= 16 ? 1 : ksw >= 8 ? 2 : 32 / ksw;
   const int nqb = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
   return nqb < cap ? nqb : cap;
 }

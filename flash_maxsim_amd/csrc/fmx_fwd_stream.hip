@@ -303,12 +303,7 @@ stream_fwd_kernel(FwdArgs a) {
         }
         if constexpr (ARGMAX) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            if (acc[r] > m[nb]) {
-              m[nb] = acc[r];
-              mi[nb] = row0 + r;
-            }
-          }
+          for (int r = 0; r < 4; ++r) argmax_fold(acc[r], row0 + r, m[nb], mi[nb]);
         } else {
           m[nb] = fold_max4(m[nb], acc[0], acc[1], acc[2], acc[3]);
         }

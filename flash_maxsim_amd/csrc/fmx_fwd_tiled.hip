@@ -77,12 +77,7 @@ __device__ __forceinline__ void fold_rows(f32x4_t acc, int rowj, int len, bool t
   }
   if constexpr (ARGMAX) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (acc[i] > m) {
-        m = acc[i];
-        mi = rowj + i;
-      }
-    }
+    for (int i = 0; i < 4; ++i) argmax_fold(acc[i], rowj + i, m, mi);
   } else {
     m = fold_max4(m, acc[0], acc[1], acc[2], acc[3]);
   }

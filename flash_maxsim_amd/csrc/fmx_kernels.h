@@ -48,9 +48,10 @@ struct BwdArgs {
   int64_t sq_n, sq_l, sd_b, sd_l, g_n, g_b;
   int Nq, B, Lq, Ld, d;
   int nchunk;                 // doc chunks of the dQ gather
-  int sort_n;                 // dD: (query, token) entries per doc padded to a power of two
-  uint32_t* dd_rows;          // dD index [B, Ld]: first sorted entry | count << 16, or ~0 (workspace)
-  uint16_t* dd_ent;           // dD index [B, Nq*Lq]: entries of each doc sorted by row (workspace)
+  int sort_n;                 // dD: entries of one index chunk padded to a power of two
+  int dd_chunks;              // dD: index chunks of kDdChunk (query, token) entries per doc
+  uint32_t* dd_rows;          // dD index [dd_chunks, B, Ld]: first sorted entry | count << 16, or ~0
+  uint16_t* dd_ent;           // dD index [B, Nq*Lq]: each chunk's entries sorted by row (chunk-local)
   int dd_slab;                // rows per dD writer workgroup
 };
 
@@ -63,7 +64,7 @@ int stream_fwd_passes(int Lq, int d, bool u8 = false); // > 1: partial sums in F
 hipError_t launch_stream_fwd(int kind, const FwdArgs& a, bool with_argmax, hipStream_t s);
 
 // Split-d kernel: the eight waves of a workgroup each own a slice of d and
-// reduce partial similarities through LDS before the max. 256 < d <= 2048.
+// reduce partial similarities through LDS before the max. 256 < d <= 4096.
 bool splitd_fwd_supported(int d);
 int splitd_fwd_ksw(int d);            // k-steps per wave
 int splitd_fwd_nqb(int Lq, int d);    // 16-token query blocks per pass
@@ -123,8 +124,10 @@ int64_t topk_ws_keys(int64_t Nq, int64_t B, int64_t k, int64_t C);
 hipError_t launch_topk(const TopkArgs& a, hipStream_t s);
 
 // dQ / dD of the argmax backward.
+constexpr int kDdChunk = 8192;                 // (query, token) entries per dD index chunk
 int bwd_dq_chunks(int B, int rows, int d);     // rows = Nq * Lq query tokens
-int bwd_sort_n(int64_t entries);               // power of two >= Nq * Lq (>= 64)
+int bwd_sort_n(int64_t entries);               // power of two >= min(Nq * Lq, kDdChunk) (>= 64)
+int64_t bwd_dd_chunks(int64_t entries);        // dD index chunks per doc
 size_t bwd_dd_lds_bytes(int64_t entries);      // dynamic LDS of the dD index kernel
 size_t bwd_dd_index_bytes(int64_t B, int64_t entries, int64_t Ld);  // its workspace
 int bwd_dd_slab(int d);                         // rows per dD writer workgroup

@@ -238,7 +238,8 @@ hipError_t dispatch_q(const QuantArgs& a, hipStream_t s) {
   if (chunks <= 32) return launch_q<SRC, 32, 1>(a, s);
   if (chunks <= 64) return launch_q<SRC, 64, 1>(a, s);
   if (chunks <= 128) return launch_q<SRC, 64, 2>(a, s);
-  return launch_q<SRC, 64, 4>(a, s);  // d <= 2048
+  if (chunks <= 256) return launch_q<SRC, 64, 4>(a, s);
+  return launch_q<SRC, 64, 8>(a, s);  // d <= 4096
 }
 
 }  // namespace

@@ -41,7 +41,7 @@ extern "C" {
 #define FMX_DTYPE_BF16 1
 #define FMX_DTYPE_F32 2 /* fmx_quantize_int8 sources only */
 
-#define FMX_MAX_D 2048
+#define FMX_MAX_D 4096
 #define FMX_MAX_TOPK 1024
 
 /* Library version string ("0.1.0+mi355x"). */
@@ -223,7 +223,7 @@ size_t fmx_bwd_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld, int64_t d);
  * autograd through the masked naive MaxSim; lengths may be NULL (= Ld).
  * dQ [Nq, Lq, d] and dD [B, Ld, d] are written contiguous in `dtype`, each
  * skipped when NULL; dD rows no token picked are zeros, picked rows are the
- * fp32 sum in (qi, q) order (deterministic). dD needs Nq*Lq < 8192, Ld < 2^19.
+ * fp32 sum in (qi, q) order (deterministic). dD needs Ld < 2^19 (any Nq*Lq).
  *
  * Generalises fmx_bwd (which is its Nq = 1, lengths = NULL case; reference
  * flash_maxsim/flash_maxsim.py:265-286) to the batched and variable-length

@@ -7,6 +7,8 @@
  *
  * Functions and the reference code they restate (roipony/flash-maxsim 0.1.0):
  *   oracle_maxsim        maxsim_naive            flash_maxsim/flash_maxsim.py:294-301
+ *                        (NaN rule of torch.max: a NaN similarity is the max,
+ *                        the first NaN its index)
  *                        + varlen mask            flash_maxsim.py:297-300, :121,:129
  *                        + argmax (first max)     flash_maxsim.py:132-135
  *                        + batched / per-query    flash_maxsim.py:94-100, :233-250
@@ -86,7 +88,10 @@ static void score_item(const job_t* J, int64_t item, float* rowbuf) {
         dv = J->D + (drow * J->Ld + j) * d;
       }
       const double s = qv ? dot_f64(qv, dv, d) : 0.0;
-      if (s > m) { /* strict: the first index reaching the max wins */
+      /* torch.max over the masked row (flash_maxsim.py:301): the first index
+       * reaching the max wins (strict); a NaN similarity is the max and the
+       * first NaN keeps it (torch.max propagates NaN and returns its index). */
+      if (m == m && !(s <= m)) {
         m = s;
         mi = (int32_t)j;
       }

@@ -8,6 +8,8 @@ fixtures are built here:
                  lengths (0, clamped, full): every score and argmax follows from
                  index arithmetic, written out by hand below.
   ties.npz       repeated doc tokens: exact ties, the first index must win.
+  nan.npz        NaN doc and query tokens (torch.max's rule: NaN is the max,
+                 the first NaN its index) and a NaN masked past a doc's length.
   quant.npz      rows on exact binary grids, a constant row (scale floor 1e-8,
                  which rounds to fp16 zero) and exact half-way codes (round half
                  to even): codes, fp16 scale and min follow by hand.
@@ -77,6 +79,39 @@ def ties_case():
     scores = np.array([4.0, 2.0])
     argmax = np.array([[0, 1, 2, 3], [0, 1, 0, 0]], np.int32)
     return dict(Q=Q, D=D, lengths=lengths, scores=scores, argmax=argmax)
+
+
+def nan_case():
+    """NaN handling of maxsim_naive's torch.max (flash_maxsim.py:301): a NaN
+    similarity is the max of its row and the first NaN's index is the argmax;
+    a NaN past a doc's length is masked to -inf first (:297-300)."""
+    B, Lq, Ld, d = 4, 4, 8, 8
+    nan = np.float32(np.nan)
+    Q = np.zeros((Lq, d), np.float32)
+    for q in range(Lq):
+        Q[q, q] = 1.0
+    D = np.zeros((B, Ld, d), np.float32)
+    for b in range(B):
+        for j in range(Ld):
+            D[b, j, j % 4] = (j + 1) / 8.0  # S[q, j] = (j + 1) / 8 when j % 4 == q, else 0
+    D[0, 5, 7] = nan                  # doc 0: token 5 is NaN against every query token
+    D[1, 6, 0] = nan                  # doc 1 (length 4): the NaN token is masked
+    D[2, 6, 3] = nan                  # doc 2: NaN tokens 3 and 6, the first is 3
+    D[2, 3, 5] = nan
+    D[3, 0, 0] = nan                  # doc 3: empty, its NaN never read
+    lengths = np.array([8, 4, 8, 0], np.int32)
+    # doc 1: S[q, q] = (q + 1) / 8 is its only nonzero: 1/8 + 2/8 + 3/8 + 4/8.
+    scores = np.array([np.nan, 1.25, np.nan, -np.inf])
+    argmax = np.array([[5] * 4, [0, 1, 2, 3], [3] * 4, [0] * 4], np.int32)
+    # A query token with a NaN (token 2) is NaN against every doc token: its
+    # argmax is the doc's first token and every non-empty doc scores NaN.
+    Qnan = Q.copy()
+    Qnan[2, 6] = nan
+    scores_qnan = np.array([np.nan, np.nan, np.nan, -np.inf])
+    argmax_qnan = argmax.copy()
+    argmax_qnan[:, 2] = 0
+    return dict(Q=Q, D=D, lengths=lengths, scores=scores, argmax=argmax, Qnan=Qnan, scores_qnan=scores_qnan,
+                argmax_qnan=argmax_qnan)
 
 
 def quant_case():
@@ -153,12 +188,15 @@ def random_small_case():
                 mins=m16, scores_int8=scores_int8[0])
 
 
-def main():
-    for name, fn in [("basis", basis_case), ("ties", ties_case), ("quant", quant_case), ("bwd", bwd_case),
-                     ("random_small", random_small_case)]:
-        np.savez(HERE / f"{name}.npz", **fn())
+CASES = {"basis": basis_case, "ties": ties_case, "nan": nan_case, "quant": quant_case, "bwd": bwd_case,
+         "random_small": random_small_case}
+
+
+def main(names=None):
+    for name in names or CASES:
+        np.savez(HERE / f"{name}.npz", **CASES[name]())
         print("wrote", HERE / f"{name}.npz")
 
 
 if __name__ == "__main__":
-    main()
+    main(sys.argv[1:])

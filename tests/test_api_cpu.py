@@ -13,6 +13,7 @@ import ctypes
 import re
 from pathlib import Path
 
+import numpy as np
 import pytest
 import torch
 
@@ -69,7 +70,7 @@ def _fwd(lib, **kw):
 
 @pytest.mark.parametrize("kw, code, text", [
     (dict(dtype=7), FMX_ERR_INVALID, "dtype"),
-    (dict(d=4096, ql=4096, dl=4096, db=4096 * 300), FMX_ERR_UNSUPPORTED, "FMX_MAX_D"),
+    (dict(d=4104, ql=4104, dl=4104, db=4104 * 300), FMX_ERR_UNSUPPORTED, "FMX_MAX_D"),
     (dict(ql=100), FMX_ERR_INVALID, "Q row stride"),
     (dict(dl=120), FMX_ERR_INVALID, "D row stride"),
     (dict(db=300 * 128 + 4), FMX_ERR_INVALID, "doc stride"),
@@ -111,6 +112,16 @@ def test_int8_and_bwd_reject_bad_arguments(lib):
     rc = lib.fmx_bwd(0, FAKE, 128, FAKE, 300 * 128, 128, FAKE, FAKE, None, None, 10, 32, 300, 128,
                      None, 0, None)
     assert rc == FMX_OK  # nothing requested
+
+
+def test_bwd_limits(lib):
+    # any Nq*Lq: the dD index runs in chunks of 8192 entries (two here)
+    assert lib.fmx_bwd_batched_workspace_bytes(70, 6, 128, 64, 128) >= 2 * 6 * 64 * 4 + 6 * 8960 * 2
+    # docs of 2^19 tokens or more are refused before any launch
+    Ld = 1 << 19
+    rc = lib.fmx_bwd_batched(0, FAKE, 0, 8, FAKE, Ld * 8, 8, None, FAKE, FAKE, 0, 1, None, FAKE, 1, 2, 4, Ld, 8,
+                             None, 0, None)
+    assert rc == FMX_ERR_UNSUPPORTED and "Ld < 2^19" in lib.fmx_last_error().decode()
 
 
 def test_sparse_rejects_bad_arguments(lib):
@@ -204,6 +215,38 @@ def test_naive_functions_run_on_cpu():
     assert fm.dequantize_int8(codes, sc, mn).shape == D.shape
     idx = torch.tensor([[0, 1], [2, 3], [3, 3]])
     assert fm.maxsim_sparse_naive(Q, D, idx).shape == (3,)
+
+
+def test_dequantize_int8_values():
+    """dequantize_int8 (reference flash_maxsim_quant.py:31-33) bit for bit:
+    against the NumPy restatement (float32 multiply, then add), against the
+    hand-derived quant fixture (codes on exact binary grids decode to the
+    original rows); fp16 arithmetic must differ somewhere."""
+    from pathlib import Path
+
+    import flash_maxsim_amd as fm
+    from oracle.oracle_np import dequantize_np
+
+    g = torch.Generator().manual_seed(5)
+    D = torch.nn.functional.normalize(torch.randn(4, 33, 96, generator=g), dim=-1) * 3.0
+    codes, sc, mn = fm.quantize_int8(D)
+    got = fm.dequantize_int8(codes, sc, mn)
+    assert got.dtype == torch.float32 and got.shape == D.shape
+    want = dequantize_np(codes.numpy(), sc.numpy(), mn.numpy())
+    np.testing.assert_array_equal(got.numpy().view(np.uint32), want.view(np.uint32))
+    # (code * step is exact in float32, 8-bit codes times 11-bit fp16 steps, so
+    # only the add rounds.) Planted mistake: the same formula in fp16
+    # arithmetic, as the reference's uint8 kernel dequantises, must differ.
+    half = (codes.numpy().astype(np.float16) * sc.numpy() + mn.numpy()).astype(np.float32)
+    assert not np.array_equal(half.view(np.uint32), got.numpy().view(np.uint32))
+    f = dict(np.load(Path(__file__).resolve().parent / "golden" / "quant.npz"))
+    rows = fm.dequantize_int8(torch.from_numpy(f["codes"]), torch.from_numpy(f["scales"]),
+                              torch.from_numpy(f["mins"])).numpy()
+    for r in (0, 3):  # exact binary grids: step and min are fp16-exact, codes decode exactly
+        np.testing.assert_array_equal(rows[0, r], f["D"][0, r])
+    # row 2: step 1/16, min 0, half-way values rounded to even codes: code / 16
+    np.testing.assert_array_equal(rows[0, 2], f["codes"][0, 2].astype(np.float32) / 16)
+    np.testing.assert_array_equal(rows[0, 1], np.full(f["D"].shape[-1], 0.5, np.float32))  # scale 0 -> min
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

@@ -100,7 +100,7 @@ def test_embedding_dims_stream(oracle_mod, d):
     assert_scores(out, ref)
 
 
-@pytest.mark.parametrize("d", [256, 512, 1024, 2048, 300, 600, 1000])
+@pytest.mark.parametrize("d", [256, 512, 1024, 2048, 300, 600, 1000, 2056, 3000, 4096])
 def test_large_embedding_dim(oracle_mod, d):
     """Reference test_large_embedding_dim (tests/test_flash_maxsim.py:58-64) plus non-power-of-2 d."""
     out, ref = run_single(oracle_mod, 20, 32, 128, d, 140 + d)
@@ -231,7 +231,7 @@ def test_int8_varlen_config4_like(oracle_mod):
     assert_scores(out, ref)
 
 
-@pytest.mark.parametrize("d", [64, 96, 100, 256, 512, 1024])
+@pytest.mark.parametrize("d", [64, 96, 100, 256, 512, 1024, 4096])
 def test_int8_dims(oracle_mod, d):
     out, ref, _ = run_int8(oracle_mod, 20, 32, 128, d, 320 + d, lengths=[128, 3, 77, 0] * 5)
     assert_scores(out, ref)
@@ -358,12 +358,6 @@ def test_train_is_deterministic():
         outs.append((s.detach().clone(), Qg.grad.clone(), Dg.grad.clone()))
     for a, b in zip(outs[0], outs[1]):
         assert torch.equal(a, b)
-
-
-def test_config5_train_sampled(oracle_mod):
-    """BASELINE config 5 shape (Q[128,1024], D[B,512,1024]) on 48 docs, loss = scores.sum()."""
-    s, dQ, dD, ref, am_ref, best, Qn, Dn, g = run_train(oracle_mod, 48, 128, 512, 1024, 5)
-    assert_scores(s, ref[0])
 
 
 def test_maxsim_naive_on_gpu(oracle_mod):

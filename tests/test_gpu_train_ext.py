@@ -79,8 +79,13 @@ def test_train_with_doc_lengths(oracle_mod, B, Lq, Ld, d):
     assert not Dg.grad[1].any()  # the empty doc gets no gradient
 
 
-@pytest.mark.parametrize("Nq, B, Lq, Ld, d", [(3, 10, 32, 60, 128), (16, 20, 32, 40, 128), (4, 6, 100, 50, 1024),
-                                              (2, 7, 24, 30, 64)])
+@pytest.mark.parametrize("Nq, B, Lq, Ld, d", [
+    (3, 10, 32, 60, 128), (16, 20, 32, 40, 128), (4, 6, 100, 50, 1024), (2, 7, 24, 30, 64),
+    # Nq*Lq >= 8192: the dD index sorts each doc's entries in chunks of 8192
+    (70, 6, 128, 64, 128),      # 8960 entries, two chunks
+    (64, 5, 300, 40, 128),      # 19200 entries, three chunks (tiled forward)
+    (70, 4, 128, 9, 64),        # 9 rows: every row's entries straddle both chunks
+])
 def test_train_batched(oracle_mod, Nq, B, Lq, Ld, d):
     Q = sim((Nq, Lq, d), 1200 + Nq)
     D = sim((B, Ld, d), 1201 + d)
@@ -138,7 +143,7 @@ def test_train_batched_deterministic_and_grad_only_q():
     assert torch.equal(Qg.grad, outs[0][0])
 
 
-@pytest.mark.parametrize("B, Lq, Ld, d", [(5, 24, 37, 20), (3, 16, 300, 2048), (40, 8, 9, 8)])
+@pytest.mark.parametrize("B, Lq, Ld, d", [(5, 24, 37, 20), (3, 16, 300, 2048), (40, 8, 9, 8), (3, 40, 50, 4096)])
 def test_train_grad_only_d(oracle_mod, B, Lq, Ld, d):
     """dD alone (Q without grad) over shapes that exercise the dD writer's
     row mapping: d % 8 != 0 (scalar stores, 16 rows per wave pass), d = 2048

@@ -42,6 +42,65 @@ def test_golden_scores_and_argmax(oracle_mod, name):
         np.testing.assert_array_equal(am[valid], f["argmax"][valid], err_msg=impl)
 
 
+def _nan_pins_hold(maxsim_fn) -> bool:
+    """True iff maxsim_fn (Q, D, lengths) -> (scores, argmax) reproduces the
+    hand-derived NaN fixture: NaN scores where a NaN similarity is read, the
+    first NaN's index as argmax, a NaN past a doc's length masked."""
+    f = load("nan")
+    for qk, sk, ak in (("Q", "scores", "argmax"), ("Qnan", "scores_qnan", "argmax_qnan")):
+        s, am = maxsim_fn(f[qk], f["D"], f["lengths"])
+        if not np.array_equal(np.reshape(s, -1), f[sk], equal_nan=True) or not np.array_equal(am, f[ak]):
+            return False
+    return True
+
+
+def test_golden_nan(oracle_mod):
+    """NaN rule of maxsim_naive's torch.max (reference flash_maxsim.py:301) in both restatements."""
+    assert _nan_pins_hold(lambda Q, D, L: oracle_mod.maxsim(Q, D, L, want_argmax=True)[:2])
+    assert _nan_pins_hold(lambda Q, D, L: oracle_np.maxsim_np(Q, D, L)[:2])
+
+
+def test_nan_rule_is_torch_max(oracle_mod):
+    """The NaN fixture through torch on the CPU: maxsim_naive's values, and
+    torch.max's indices over the same masked similarities."""
+    from flash_maxsim_amd import maxsim_naive
+
+    f = load("nan")
+    L = torch.from_numpy(f["lengths"])
+    for qk, sk, ak in (("Q", "scores", "argmax"), ("Qnan", "scores_qnan", "argmax_qnan")):
+        Q, D = torch.from_numpy(f[qk]), torch.from_numpy(f["D"])
+        np.testing.assert_array_equal(maxsim_naive(Q, D, L).double().numpy(), f[sk])
+        S = torch.matmul(D, Q.t())
+        S = S.masked_fill(torch.arange(D.shape[1])[None, :, None] >= L[:, None, None], float("-inf"))
+        idx = S.max(dim=1).indices.numpy()
+        valid = f["lengths"] > 0
+        np.testing.assert_array_equal(idx[valid], f[ak][valid])
+
+
+def test_nan_pins_reject_nan_skipping_max():
+    """Planted mistake: a max that skips NaN (strict > from -inf, i.e. nanmax
+    with its first index) must fail the NaN pins."""
+    def skip_nan(Q, D, lengths):
+        Q, D = np.asarray(Q, np.float64), np.asarray(D, np.float64)
+        B, Ld, _ = D.shape
+        scores, argmax = np.empty(B), np.zeros((B, Q.shape[0]), np.int32)
+        for b in range(B):
+            n = min(max(int(lengths[b]), 0), Ld)
+            tot = 0.0
+            for q in range(Q.shape[0]):
+                m, mi = -np.inf, 0
+                for j in range(n):
+                    s = float(Q[q] @ D[b, j])
+                    if s > m:
+                        m, mi = s, j
+                tot += m
+                argmax[b, q] = mi
+            scores[b] = tot
+        return scores, argmax
+
+    assert not _nan_pins_hold(skip_nan)
+
+
 def test_golden_quant(oracle_mod):
     from flash_maxsim_amd import quantize_int8
 
