@@ -33,6 +33,11 @@ _SIGNATURES = {
          _i64, _i64, _i64, _i64, _i64, _int, _ptr, _size, _ptr],
     ),
     "fmx_fwd_workspace_bytes": (_size, [_i64, _i64, _i64, _i64, _i64]),
+    "fmx_fwd_noalloc": (
+        _int,
+        [_int, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i64, _ptr,
+         _i64, _i64, _i64, _i64, _i64, _int, _ptr],
+    ),
     "fmx_fwd_int8": (
         _int,
         [_ptr, _i64, _ptr, _i64, _i64, _ptr, _ptr, _i64, _ptr, _ptr,

@@ -3,6 +3,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
 #include <string>
 
 #include "../../include/fmx.h"
@@ -111,6 +112,39 @@ int hip_status(hipError_t e, const char* what) {
 
 }  // namespace
 
+// Scratch of fmx_fwd_noalloc: a static device array, one copy per GPU, held
+// until the process ends. Its name is a host-side stand-in, never a device
+// address: host code uses only the per-device address hipGetSymbolAddress
+// returns (scratch_address).
+static __device__ __align__(256) unsigned char scratch[FMX_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up on the first call on
+// that device (with it current) and kept.
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(FMX_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(FMX_ERR_UNSUPPORTED, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(FMX_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return FMX_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* fmx_version(void) { return "0.1.0+mi355x"; }
@@ -135,7 +169,8 @@ namespace {
 int fwd_impl(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, const void* D, int64_t d_stride_b,
              int64_t d_stride_l, const int64_t* tok_group, int64_t tok_rows, const int32_t* lengths, float* scores,
              int64_t s_stride_n, int64_t s_stride_b, int32_t* argmax, int64_t Nq, int64_t B, int64_t Lq, int64_t Ld,
-             int64_t d, int shared_docs, void* workspace, size_t workspace_bytes, void* stream) {
+             int64_t d, int shared_docs, void* workspace, size_t workspace_bytes, void* stream,
+             bool noalloc = false) {
   if (dtype != FMX_DTYPE_F16 && dtype != FMX_DTYPE_BF16) return fail(FMX_ERR_INVALID, "unknown dtype %d", dtype);
   int rc = check_common(Nq, B, Lq, Ld, d, q_stride_l, d_stride_b, d_stride_l, 2);
   if (rc) return rc;
@@ -151,6 +186,19 @@ int fwd_impl(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, c
     need = fmx::tiled_fwd_workspace_bytes(tp, Nq, B);
   } else {
     need = stream_ws_bytes(Nq, B, Lq, d);
+  }
+  if (noalloc) {
+    // the static scratch array stands in for the workspace
+    if (need > FMX_NOALLOC_SCRATCH_BYTES)
+      return fail(FMX_ERR_UNSUPPORTED, "scratch of %zu bytes required, FMX_NOALLOC_SCRATCH_BYTES is %zu", need,
+                  (size_t)FMX_NOALLOC_SCRATCH_BYTES);
+    workspace = nullptr;
+    workspace_bytes = 0;
+    if (need > 0) {
+      rc = scratch_address(&workspace);
+      if (rc) return rc;
+      workspace_bytes = FMX_NOALLOC_SCRATCH_BYTES;
+    }
   }
   if (need > 0 && (!workspace || workspace_bytes < need))
     return fail(FMX_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
@@ -272,6 +320,14 @@ int fmx_fwd_int8(const void* Q, int64_t q_stride_l, const uint8_t* D, int64_t d_
                  void* workspace, size_t workspace_bytes, void* stream) {
   return int8_impl(Q, q_stride_l, D, d_stride_b, d_stride_l, scales, mins, sm_stride_b, nullptr, 0, lengths, scores,
                    B, Lq, Ld, d, workspace, workspace_bytes, stream);
+}
+
+int fmx_fwd_noalloc(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, const void* D,
+                    int64_t d_stride_b, int64_t d_stride_l, const int32_t* lengths, float* scores,
+                    int64_t s_stride_n, int64_t s_stride_b, int32_t* argmax, int64_t Nq, int64_t B,
+                    int64_t Lq, int64_t Ld, int64_t d, int shared_docs, void* stream) {
+  return fwd_impl(dtype, Q, q_stride_n, q_stride_l, D, d_stride_b, d_stride_l, nullptr, 0, lengths, scores,
+                  s_stride_n, s_stride_b, argmax, Nq, B, Lq, Ld, d, shared_docs, nullptr, 0, stream, true);
 }
 
 size_t fmx_fwd_packed_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld_max, int64_t d) {

@@ -43,6 +43,7 @@ extern "C" {
 
 #define FMX_MAX_D 4096
 #define FMX_MAX_TOPK 1024
+#define FMX_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20) /* per GPU, see fmx_fwd_noalloc */
 
 /* Library version string ("0.1.0+mi355x"). */
 const char* fmx_version(void);
@@ -74,6 +75,25 @@ int fmx_fwd(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, co
             size_t workspace_bytes, void* stream);
 
 size_t fmx_fwd_workspace_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t Ld, int64_t d);
+
+/*
+ * fmx_fwd for callers that cannot allocate: code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc. No counterpart in the
+ * reference. Same arguments, results and errors as fmx_fwd without the
+ * workspace: the partial sums fmx_fwd keeps in its workspace (queries that
+ * take several passes, queries straddling row blocks) go to a static device
+ * array of FMX_NOALLOC_SCRATCH_BYTES on each GPU, held until the process
+ * ends. A call whose fmx_fwd_workspace_bytes exceeds that fails with
+ * FMX_ERR_UNSUPPORTED before any launch. The call allocates nothing (no
+ * hipMalloc, no allocating library routine); its first call on a GPU looks up
+ * that GPU's copy of the array. Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (other streams, other threads) race, and must
+ * be ordered by the caller. Nothing in the array needs to start at zero.
+ */
+int fmx_fwd_noalloc(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, const void* D,
+                    int64_t d_stride_b, int64_t d_stride_l, const int32_t* lengths, float* scores,
+                    int64_t s_stride_n, int64_t s_stride_b, int32_t* argmax, int64_t Nq, int64_t B,
+                    int64_t Lq, int64_t Ld, int64_t d, int shared_docs, void* stream);
 
 /*
  * Fused uint8-dequant MaxSim forward: doc token j of doc b is

@@ -85,6 +85,17 @@ def test_fwd_rejects_bad_arguments(lib, kw, code, text):
     assert text in lib.fmx_last_error().decode()
 
 
+def test_noalloc_rejects_scratch_overflow(lib):
+    # 100 queries of 1024 tokens over 10000 per-query docs: 8 passes of partial
+    # sums, 32 MB, beyond the 16 MiB static scratch; refused before any launch.
+    need = lib.fmx_fwd_workspace_bytes(100, 10000, 1024, 300, 128)
+    assert need == 8 * 100 * 10000 * 4 > (16 << 20)
+    rc = lib.fmx_fwd_noalloc(0, FAKE, 1024 * 128, 128, FAKE, 300 * 128, 128, None, FAKE, 10000, 1, None,
+                             100, 10000, 1024, 300, 128, 0, None)
+    assert rc == FMX_ERR_UNSUPPORTED
+    assert "FMX_NOALLOC_SCRATCH_BYTES" in lib.fmx_last_error().decode()
+
+
 def test_fwd_empty_batch_is_a_no_op(lib):
     assert _fwd(lib, B=0, Q=None, D=None, scores=None) == FMX_OK
     assert lib.fmx_last_error().decode() == ""
