@@ -330,6 +330,46 @@ int fmx_fwd_noalloc(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stri
                   s_stride_n, s_stride_b, argmax, Nq, B, Lq, Ld, d, shared_docs, nullptr, 0, stream, true);
 }
 
+}  // extern "C"
+
+namespace {
+
+// fmx_fwd_topk's workspace: fmx_fwd's, then fmx_topk's (256-byte aligned).
+size_t topk_fwd_part(int64_t B, int64_t Lq, int64_t d) { return (fwd_ws_bytes(1, B, Lq, d) + 255) & ~(size_t)255; }
+
+}  // namespace
+
+extern "C" {
+
+size_t fmx_fwd_topk_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld, int64_t d, int64_t k) {
+  (void)Ld;
+  if (B < 1 || Lq < 1 || d < 1 || d > FMX_MAX_D || k < 1) return 0;
+  return topk_fwd_part(B, Lq, d) + fmx_topk_workspace_bytes(1, B, k);
+}
+
+int fmx_fwd_topk(int dtype, const void* Q, int64_t q_stride_l, const void* D, int64_t d_stride_b,
+                 int64_t d_stride_l, const int32_t* lengths, int64_t B, int64_t Lq, int64_t Ld, int64_t d,
+                 int64_t k, float* scores, float* values, int64_t* indices, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  if (k < 0 || B < 0) return fail(FMX_ERR_INVALID, "invalid sizes B=%lld k=%lld", (long long)B, (long long)k);
+  if (k > B) return fail(FMX_ERR_INVALID, "k=%lld exceeds the %lld scores", (long long)k, (long long)B);
+  if (k > FMX_MAX_TOPK) return fail(FMX_ERR_UNSUPPORTED, "k=%lld exceeds FMX_MAX_TOPK=%d", (long long)k, FMX_MAX_TOPK);
+  int rc = check_common(1, B, Lq, Ld, d, q_stride_l, d_stride_b, d_stride_l, 2);
+  if (rc) return rc;
+  if (k > 0 && (!values || !indices)) return fail(FMX_ERR_INVALID, "values and indices must be non-null");
+  const size_t need = fmx_fwd_topk_workspace_bytes(B, Lq, Ld, d, k);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(FMX_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255u) return fail(FMX_ERR_INVALID, "workspace must be 256-byte aligned");
+  char* w = static_cast<char*>(workspace);
+  const size_t fws = B > 0 ? topk_fwd_part(B, Lq, d) : 0;
+  rc = fmx_fwd(dtype, Q, 0, q_stride_l, D, d_stride_b, d_stride_l, lengths, scores, 0, 1, nullptr, 1, B, Lq, Ld, d, 1,
+               fws ? w : nullptr, fws, stream);
+  if (rc || B == 0 || k == 0) return rc;
+  const size_t tws = fmx_topk_workspace_bytes(1, B, k);
+  return fmx_topk(scores, B, 1, B, k, values, indices, k, tws ? w + fws : nullptr, tws, stream);
+}
+
 size_t fmx_fwd_packed_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld_max, int64_t d) {
   return fwd_ws_bytes(1, B, Lq, d);
 }

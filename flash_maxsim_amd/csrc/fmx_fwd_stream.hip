@@ -175,8 +175,8 @@ stream_fwd_kernel(FwdArgs a) {
   }
   // Sequence position -> (doc, tile of that doc); uniform over the wave.
   // Positions past the sequence read an empty range (zeros, no memory access).
-  constexpr bool FIXED = U8;  // fixed refill pattern (below)
-  constexpr bool GSM = FIXED && VEC;  // group scale loads (below)
+  constexpr bool FIXED = !ARGMAX;  // fixed refill pattern (below)
+  constexpr bool GSM = U8 && VEC;  // group scale loads (below)
   static_assert(!GSM || P == 4, "group scale loads map 16 lanes per tile slot");
   static_assert(!JOINT || (GSM && DOCS == 2), "a joint scale range serves two-doc group loads");
   const rsrc_t nul = make_rsrc(a.D, 0u);
@@ -332,9 +332,11 @@ stream_fwd_kernel(FwdArgs a) {
     // A fixed load pattern: every group of P tiles that has a next group
     // refills all P slots, so the compiler's wait before each tile counts the
     // P-1 tiles still in flight behind it (a conditional load makes it wait
-    // for all of them). The empty-range loads past the end cost issue slots;
-    // fp16/bf16 waves (4-5 tiles each at config 1) lose more to those than
-    // they gain, uint8 waves (two docs, ~16 tiles) gain.
+    // for all of them). The empty-range loads past the end cost issue slots,
+    // which long docs amortise (Q[128,128] x 1024-token docs: 52.7 -> 49.4 us)
+    // and short ones no longer lose (config 1: 61.2 -> 60.9 us). The argmax
+    // instances keep conditional loads: the fixed pattern's registers cost
+    // them a wave per SIMD.
     int i0 = 0;
     for (; i0 + P < my_n; i0 += P) {
       if constexpr (GSM) group_sm(i0 + P, gsn, gmn);

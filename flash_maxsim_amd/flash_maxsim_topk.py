@@ -16,9 +16,9 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .flash_maxsim import _check_devices, _device_guard, flash_maxsim, flash_maxsim_batched
+from .flash_maxsim import (_check_devices, _device_guard, _kernel_dtype, _lengths, _prep, flash_maxsim,
+                           flash_maxsim_batched)
 from .flash_maxsim_quant import flash_maxsim_int8
-
 
 def topk_scores(scores: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Tensor]:
     """(values fp32, indices int64) of the k best entries of each row of
@@ -48,8 +48,35 @@ def topk_scores(scores: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Tenso
 
 
 def flash_maxsim_topk(Q: torch.Tensor, D: torch.Tensor, k: int, doc_lengths=None):
-    """The k best docs for one query: (scores fp32 [k], doc indices int64 [k])."""
-    return topk_scores(flash_maxsim(Q, D, doc_lengths), k)
+    """The k best docs for one query: (scores fp32 [k], doc indices int64 [k]).
+
+    One call of fmx_fwd_topk (the scoring and the selection kernels back to
+    back); the results equal topk_scores(flash_maxsim(Q, D), k).
+    """
+    assert Q.ndim == 2 and D.ndim == 3 and Q.size(1) == D.size(2)
+    Lq, d = Q.shape
+    B, Ld = D.shape[:2]
+    if not 0 <= k <= B:
+        raise ValueError(f"k={k} must be in [0, {B}]")
+    if Lq == 0 or k == 0:
+        return topk_scores(flash_maxsim(Q, D, doc_lengths), k)
+    kdt = _kernel_dtype(Q, D)
+    lengths = _lengths(B, D.device, doc_lengths)
+    Qk, Dk = _prep(Q, kdt), _prep(D, kdt)
+    dev = _check_devices(Qk, Dk, lengths)
+    scores = torch.empty(B, device=dev, dtype=torch.float32)
+    values = torch.empty(k, device=dev, dtype=torch.float32)
+    indices = torch.empty(k, device=dev, dtype=torch.int64)
+    lib = _lib.load()
+    with _device_guard(dev):
+        stream = _lib.stream_of(Qk)
+        nbytes = lib.fmx_fwd_topk_workspace_bytes(B, Lq, Ld, d, k)
+        ws = _lib.workspace(nbytes, dev)
+        rc = lib.fmx_fwd_topk(_lib.dtype_code(Qk), Qk.data_ptr(), Qk.stride(0), Dk.data_ptr(), Dk.stride(0),
+                              Dk.stride(1), _lib.ptr(lengths), B, Lq, Ld, d, k, scores.data_ptr(), values.data_ptr(),
+                              indices.data_ptr(), _lib.ptr(ws), nbytes, stream)
+    _lib.check(rc)
+    return values, indices
 
 
 def flash_maxsim_batched_topk(Q: torch.Tensor, D: torch.Tensor, k: int, doc_lengths=None,

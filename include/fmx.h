@@ -209,6 +209,24 @@ int fmx_topk(const float* scores, int64_t s_stride_n, int64_t Nq, int64_t B, int
 size_t fmx_topk_workspace_bytes(int64_t Nq, int64_t B, int64_t k);
 
 /*
+ * Single-query scoring and top-k in one call: scores[b] as fmx_fwd (Nq = 1,
+ * shared docs, contiguous scores [B]), then values [k] / indices [k] as
+ * fmx_topk over them, back to back on the stream. Workspace:
+ * fmx_fwd_topk_workspace_bytes bytes, 256-byte aligned (or NULL when that is
+ * 0).
+ *
+ * No counterpart in the reference: its callers rank flash_maxsim's scores
+ * themselves (torch topk / argsort: benchmarks/bench.py:36,
+ * examples/demo.py:127-128, tests/test_flash_maxsim.py:87-88).
+ */
+int fmx_fwd_topk(int dtype, const void* Q, int64_t q_stride_l, const void* D, int64_t d_stride_b,
+                 int64_t d_stride_l, const int32_t* lengths, int64_t B, int64_t Lq, int64_t Ld, int64_t d,
+                 int64_t k, float* scores, float* values, int64_t* indices, void* workspace,
+                 size_t workspace_bytes, void* stream);
+
+size_t fmx_fwd_topk_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld, int64_t d, int64_t k);
+
+/*
  * Argmax backward of the single-query forward (argmax from fmx_fwd, Nq = 1):
  *   dQ[q, :]    = sum_b grad[b] * D[b, argmax[b, q], :]
  *   dD[b, j, :] = grad[b] * sum_{q : argmax[b, q] = j} Q[q, :]

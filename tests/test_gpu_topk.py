@@ -86,3 +86,99 @@ def test_fused_retrieval_calls(oracle_mod):
     vi, ii = fm.flash_maxsim_int8_topk(Q.to(DEV), codes, sc, mn, 9, lengths.to(DEV))
     si = fm.flash_maxsim_int8(Q.to(DEV), codes, sc, mn, lengths.to(DEV))
     assert_same_selection((vi, ii), oracle_mod.topk(si.cpu().numpy(), 9))
+
+
+# ------------------------------------ one-call scoring + selection ----
+
+def _topk_inputs(B, Lq, d, dtype, seed):
+    """Docs with exact ties (copies of doc 3), a NaN doc and empty docs."""
+    Q = sim((Lq, d), seed, dtype)
+    D = sim((B, 24, d), seed + 1, dtype)
+    if B > 12:
+        D[5::9] = D[3]                   # identical docs: equal scores, smaller index first
+        D[11, 0, 0] = float("nan")       # a NaN score ranks first
+    lengths = torch.randint(1, 25, (B,), generator=torch.Generator().manual_seed(seed), dtype=torch.int32)
+    if B > 12:
+        lengths[5::9] = lengths[3]
+        lengths[11] = 24
+        lengths[7::13] = 0               # empty docs score -inf
+    return Q.to(DEV), D.to(DEV), lengths.to(DEV)
+
+
+@pytest.mark.parametrize("B, k, Lq, d, dtype", [
+    (1, 1, 32, 128, torch.float16),
+    (2, 2, 32, 128, torch.float16),      # k == B
+    (255, 17, 32, 128, torch.float16),
+    (257, 128, 16, 64, torch.float16),
+    (5000, 100, 32, 128, torch.float16),  # config 1 + top-100
+    (8192, 128, 32, 128, torch.float16),
+    (4000, 50, 64, 256, torch.bfloat16),  # d = 256 in one pass
+    (20000, 100, 32, 128, torch.float16),  # two selection levels
+    (3000, 700, 32, 128, torch.float16),   # large k
+    (2000, 30, 65, 256, torch.float16),    # two streaming passes (workspace)
+    (1000, 40, 200, 128, torch.float16),   # tiled kernel
+])
+def test_one_call_topk_equals_selection_of_scores(oracle_mod, B, k, Lq, d, dtype):
+    """flash_maxsim_topk (fmx_fwd_topk) returns exactly the oracle's selection
+    over flash_maxsim's scores (the same kernel, bit-identical scores), call
+    after call."""
+    Q, D, L = _topk_inputs(B, Lq, d, dtype, B + k + Lq)
+    s = fm.flash_maxsim(Q, D, L)
+    want = oracle_mod.topk(s.cpu().numpy(), k)
+    for _ in range(3):
+        assert_same_selection(fm.flash_maxsim_topk(Q, D, k, L), want)
+    if B > 12:
+        v, i = fm.flash_maxsim_topk(Q, D, k, L)
+        assert torch.isnan(v[0]) and i[0].item() == 11
+
+
+def test_one_call_topk_alternating_sizes_one_stream(oracle_mod):
+    """Calls of different sizes back to back on one stream."""
+    cases = [(5000, 100), (300, 7), (5000, 1), (64, 64), (2047, 128), (8000, 300)]
+    inputs = [_topk_inputs(B, 32, 128, torch.float16, 7 * B + k) for B, k in cases]
+    wants = [oracle_mod.topk(fm.flash_maxsim(Q, D, L).cpu().numpy(), k) for (Q, D, L), (B, k) in zip(inputs, cases)]
+    outs = [fm.flash_maxsim_topk(Q, D, k, L) for (Q, D, L), (B, k) in zip(inputs, cases)]
+    outs += [fm.flash_maxsim_topk(Q, D, k, L) for (Q, D, L), (B, k) in zip(inputs, cases)]
+    for j, got in enumerate(outs):
+        assert_same_selection(got, wants[j % len(cases)])
+
+
+def test_one_call_topk_graph_replays(oracle_mod):
+    """Under HIP graph capture the one-call retrieval replays correctly, with
+    eager work in between the replays."""
+    Q, D, L = _topk_inputs(5000, 32, 128, torch.float16, 4242)
+    want = oracle_mod.topk(fm.flash_maxsim(Q, D, L).cpu().numpy(), 100)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fm.flash_maxsim_topk(Q, D, 100, L)  # warm-up on the capture stream
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        v, i = fm.flash_maxsim_topk(Q, D, 100, L)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert_same_selection((v, i), want)
+        eager = fm.flash_maxsim_topk(Q, D, 100, L)  # eager work between replays
+        torch.cuda.synchronize()
+        assert_same_selection(eager, want)
+
+
+def test_one_call_topk_many_calls(oracle_mod):
+    """300 calls over four inputs, each result checked."""
+    cases = [(5000, 100, 32), (8192, 128, 16), (1200, 33, 128), (3001, 5, 64)]
+    inputs = [_topk_inputs(B, Lq, 128, torch.float16, 31 * B + k) for B, k, Lq in cases]
+    wants = []
+    for (Q, D, L), (B, k, Lq) in zip(inputs, cases):
+        v, i = oracle_mod.topk(fm.flash_maxsim(Q, D, L).cpu().numpy(), k)
+        wants.append((torch.from_numpy(np.asarray(v)).to(DEV), torch.from_numpy(np.asarray(i)).to(DEV)))
+    bad = 0
+    for n in range(300):
+        j = n % len(cases)
+        Q, D, L = inputs[j]
+        v, i = fm.flash_maxsim_topk(Q, D, cases[j][1], L)
+        wv, wi = wants[j]
+        same = torch.equal(i, wi) and torch.equal(v.view(torch.int32), wv.view(torch.int32))
+        bad += 0 if same else 1
+    assert bad == 0, f"{bad} of 300 selections differ"
