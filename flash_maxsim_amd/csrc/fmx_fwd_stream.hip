@@ -45,9 +45,10 @@ constexpr int stream_depth() { return (KIND != KIND_U8 && KS >= 8) ? 2 : 4; }
 // 2x and 2x+1 as one tile sequence (the first doc's tiles, then the second's),
 // so its query tile, row sums and load ring carry over from one doc to the
 // next instead of being rebuilt and refilled per doc.
-// JOINT (two padded uint8 docs with aligned rows): the pair's scale rows are
-// adjacent, so one buffer range covers both and the group scale loads (below)
-// take one instruction per array instead of one per doc.
+// JOINT (two uint8 docs with aligned rows): one buffer range covers the
+// pair's scale rows (padded: adjacent rows; packed: wherever the two token
+// groups start), so the group scale loads (below) take one instruction per
+// array instead of one per doc.
 // Waves per SIMD asked of the compiler: three for the one-doc uint8 instance
 // of 64 query rows (the passes of longer queries; 188 VGPRs allowed two, and
 // fitting 168 costs one spill: Lq = 128 139 -> 125 us). The two-doc instance
@@ -200,10 +201,34 @@ stream_fwd_kernel(FwdArgs a) {
   // rows from those lanes. The stream issues a quarter fewer load
   // instructions, which is what bounds it.
   rsrc_t rsj = nul, rmj = nul;  // JOINT: scale / min rows of both docs
+  uint32_t jo0 = 0u, jo1 = kOOB;  // byte offset of each doc's rows in them (kOOB: none)
   if constexpr (JOINT) {
-    const int64_t span = two ? a.sm_b + ((len1 + 3) & ~3) : ((len0 + 3) & ~3);
-    rsj = make_rsrc(a.scales + drow * a.sm_b, (uint32_t)(span * 2));
-    rmj = make_rsrc(a.mins + drow * a.sm_b, (uint32_t)(span * 2));
+    int64_t lo, hi;  // token rows of the scale arrays the range covers
+    if (a.tok_group) {
+      // Packed docs: each doc's rows (its length rounded up to 4, within the
+      // tokens of D) wherever its token group starts; the range spans both.
+      const int64_t t0 = 4 * tok_group_of(a, drow), t1 = two ? 4 * tok_group_of(a, drow + 1) : t0;
+      auto rows_at = [&](int64_t t, int len) {
+        const int64_t avail = t < 0 ? 0 : (a.tok_rows > t ? a.tok_rows - t : 0);
+        const int64_t n = (len + 3) & ~3;
+        return n < avail ? n : avail;
+      };
+      const int64_t n0 = rows_at(t0, len0), n1 = two ? rows_at(t1, len1) : 0;
+      lo = n0 ? t0 : (n1 ? t1 : 0);
+      if (n1 && t1 < lo) lo = t1;
+      hi = lo;
+      if (n0 && t0 + n0 > hi) hi = t0 + n0;
+      if (n1 && t1 + n1 > hi) hi = t1 + n1;
+      jo0 = n0 ? (uint32_t)((t0 - lo) * 2) : kOOB;
+      jo1 = n1 ? (uint32_t)((t1 - lo) * 2) : kOOB;
+    } else {
+      // Padded docs: doc 1's rows start sm_b tokens after doc 0's.
+      lo = drow * a.sm_b;
+      hi = lo + (two ? a.sm_b + ((len1 + 3) & ~3) : ((len0 + 3) & ~3));
+      jo1 = (uint32_t)(a.sm_b * 2);
+    }
+    rsj = make_rsrc(a.scales + lo, (uint32_t)((hi - lo) * 2));
+    rmj = make_rsrc(a.mins + lo, (uint32_t)((hi - lo) * 2));
   }
   auto group_sm = [&](int ig, uint32_t& gs, uint32_t& gm) {
     const int sq = wave + NW * (ig + (lane >> 4));
@@ -211,8 +236,8 @@ stream_fwd_kernel(FwdArgs a) {
     const bool in1 = DOCS == 2 && sq >= nt0;
     const uint32_t off = (uint32_t)((in1 ? sq - nt0 : sq) * 32 + (lane & 7) * 4);
     if constexpr (JOINT) {
-      // doc 1's rows start sm_b tokens after doc 0's
-      const uint32_t o = past ? kOOB : (in1 ? (uint32_t)(a.sm_b * 2) + off : off);
+      // a doc without rows in the range reads zeros (kOOB + off stays past it)
+      const uint32_t o = past ? kOOB : (in1 ? jo1 : jo0) + off;
       gs = ld4(rsj, o);
       gm = ld4(rmj, o);
     } else if constexpr (DOCS == 2) {
@@ -440,8 +465,10 @@ hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
     // uint8 docs of one query in one pass: two docs per workgroup.
     if (a.Nq == 1 && npass == 1 && !a.qidx) {
       const dim3 grid((unsigned)((a.B + 1) / 2));
-      // Padded docs whose pair of scale rows stays within the 2^31-byte range.
-      if (VEC && !a.tok_group && (a.sm_b + a.Ld) * 2 + 64 < ((int64_t)1 << 31)) {
+      // One scale range per pair when its offsets stay below 2^31 bytes: a
+      // pair of padded scale rows, or the whole packed scale array.
+      const int64_t sm_rows = a.tok_group ? a.tok_rows : a.sm_b + a.Ld;
+      if (VEC && sm_rows * 2 + 64 < ((int64_t)1 << 31)) {
         hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2, VEC>), grid, dim3(256), 0, s, a);
       } else {
         hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2>), grid, dim3(256), 0, s, a);

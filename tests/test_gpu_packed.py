@@ -142,6 +142,31 @@ def test_int8_packed_groups_in_any_order():
     np.testing.assert_array_equal(got.cpu().numpy(), want.cpu().numpy())
 
 
+@pytest.mark.parametrize("cut", [0.3, 0.77])
+def test_int8_packed_docs_cut_by_tok_rows(oracle_mod, cut):
+    """Token rows at or past tok_rows read as zeros (codes, scales and mins),
+    so a doc's tokens there score 0: docs wholly past the end, docs that
+    straddle it, in both members of the two-doc workgroups."""
+    B, Ld, d, Lq = 41, 70, 128, 32
+    Q = sim((Lq, d), 75)
+    x = sim((B, Ld, d), 76, torch.float32)
+    lengths = torch.randint(1, Ld + 1, (B,), generator=torch.Generator().manual_seed(9), dtype=torch.int32)
+    packed = fm.quantize_int8_packed(x.to(DEV), lengths.to(DEV))
+    T = int(cut * packed.codes.shape[0])
+    cut_docs = fm.PackedInt8Docs(packed.codes[:T], packed.scales[:T], packed.mins[:T], packed.tok_group,
+                                 packed.lengths, packed.max_len)
+    got = fm.flash_maxsim_int8_packed(Q.to(DEV), cut_docs).double().cpu().numpy()
+    codes, s16, m16, _ = oracle_mod.quantize_int8(to_np32(x))
+    s32, m32 = s16.astype(np.float32).reshape(B, Ld), m16.astype(np.float32).reshape(B, Ld)
+    tg = packed.tok_group.cpu().numpy()
+    rows = 4 * tg[:, None] + np.arange(Ld)[None, :]
+    gone = rows >= T
+    assert gone.any(axis=1).sum() >= 2 and (~gone).any(axis=1).sum() >= 2
+    codes[gone], s32[gone], m32[gone] = 0, 0.0, 0.0
+    ref = oracle_mod.maxsim_int8(to_np32(Q), codes, s32, m32, lengths.numpy())
+    assert np.abs(got - ref).max() <= ATOL
+
+
 @pytest.mark.parametrize("Lq, d, dtype", [(32, 128, torch.float16), (300, 128, torch.float16),
                                           (32, 1024, torch.float16), (20, 96, torch.bfloat16)])
 def test_packed_scores(oracle_mod, Lq, d, dtype):
