@@ -4,7 +4,7 @@ Default workload (BASELINE metric): single-query MaxSim, Q[32,128] against
 D[5000,300,128] fp16 (reference flash_maxsim(Q, D)), inputs resident in HBM.
 A step is one flash_maxsim call over the whole batch. value = docs/s.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME] [--rotate R] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME] [--rotate R] [--doc-align A] [--no-cpu]
 
 Configs (the driver's line is the default, c1):
   c1         metric workload, config 1 at B = 5000
@@ -24,6 +24,7 @@ Configs (the driver's line is the default, c1):
   quant      quantize_int8 of config 4's docs (fp16 source) on the GPU
   copy       a device copy of 384 MB, to calibrate HBM byte counters
 --rotate R (R >= 2) cycles R copies of the doc tensor(s) for any config.
+--doc-align A (c4_packed) starts each packed doc on a multiple of A token rows.
 
 roofline: the dominant kernel's algorithmic bytes (or flops) per launch divided
 by its average launch duration, timed with HIP events recorded on the stream
@@ -92,7 +93,29 @@ def _copies(t, rotate):
     return [t] + [t.clone() for _ in range(max(1, rotate) - 1)]
 
 
-def build(name: str, rotate: int) -> Workload:
+def _realign(packed, align: int):
+    """The same packed docs with each doc's rows starting on a multiple of
+    `align` token rows (gaps of zero rows between docs)."""
+    import torch
+
+    import flash_maxsim_amd as fm
+
+    L = packed.lengths.to(torch.int64)
+    n = (L + align - 1) // align * align
+    start = torch.cumsum(n, 0) - n
+    T = int(n.sum())
+    j = torch.arange(int(L.max()), device=L.device)
+    keep = j[None, :] < L[:, None]
+    src = (4 * packed.tok_group[:, None] + j[None, :])[keep]
+    dst = (start[:, None] + j[None, :])[keep]
+    codes = torch.zeros(T, packed.codes.shape[1], dtype=packed.codes.dtype, device=L.device)
+    scales = torch.zeros(T, dtype=packed.scales.dtype, device=L.device)
+    mins = torch.zeros(T, dtype=packed.mins.dtype, device=L.device)
+    codes[dst], scales[dst], mins[dst] = packed.codes[src], packed.scales[src], packed.mins[src]
+    return fm.PackedInt8Docs(codes, scales, mins, (start // 4).contiguous(), packed.lengths, packed.max_len)
+
+
+def build(name: str, rotate: int, doc_align: int = 4) -> Workload:
     import torch
 
     import flash_maxsim_amd as fm
@@ -219,12 +242,16 @@ def build(name: str, rotate: int) -> Workload:
                 Dg[b0:b0 + 500] = sim((500, Ld, d), 42 + b0, torch.float32, dev)
             packed = fm.quantize_int8_packed(Dg, lengths)
             del Dg, codes, scales, mins
+            if doc_align > 4:
+                packed = _realign(packed, doc_align)
             packs = [packed] + [fm.PackedInt8Docs(packed.codes.clone(), packed.scales.clone(), packed.mins.clone(),
                                                   packed.tok_group, packed.lengths, packed.max_len)
                                 for _ in range(max(1, rotate) - 1)]
             cfg = {"workload": f"int8 packed varlen flash_maxsim_int8_packed Q[{Lq},{d}] x {B} docs of "
                                f"U[32,1024] tokens, d={d} u8 ({packed.codes.shape[0]} packed rows)", "B": B,
                    "Lq": Lq, "d": d, "sum_len": tot}
+            if doc_align > 4:
+                cfg["doc_align_rows"] = doc_align
             steps = [lambda p=p: fm.flash_maxsim_int8_packed(Qd, p) for p in packs]
             algo = tot * (d + 4) + Lq * d * 2 + B * 16  # + tok_group, lengths, scores
         else:
@@ -328,17 +355,21 @@ def main():
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--config", default="c1", help="workload name (see the module docstring)")
     ap.add_argument("--rotate", type=int, default=1, help="cycle this many copies of the docs")
+    ap.add_argument("--doc-align", type=int, default=4,
+                    help="c4_packed: start each packed doc on a multiple of this many token rows (4 = packed)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: every GPU box of this build has one MI355X, and the "
-              "multi-GPU path (docs sharded across GPUs) is described in DESIGN.md, not run.", file=sys.stderr)
+        print("bench.py measures one GPU: every GPU box of this build has one MI355X; sharding docs "
+              "across GPUs is a design here, not a run.", file=sys.stderr)
         raise SystemExit(2)
 
     import torch
 
     torch.cuda.set_device(0)
-    w = build(args.config, args.rotate)
+    if args.doc_align < 4 or args.doc_align % 4:
+        raise SystemExit("--doc-align must be a positive multiple of 4")
+    w = build(args.config, args.rotate, args.doc_align)
     steps = w.steps
     for i in range(args.warmup):
         steps[i % len(steps)]()
@@ -370,7 +401,7 @@ def main():
     else:
         achieved /= 1e12
         peak = MFMA_F16_PEAK_TFLOPS
-    traffic, traffic_src = measured_traffic(args.config)
+    traffic, traffic_src = measured_traffic(args.config) if args.doc_align == 4 else (None, None)
     roofline = {"bound": roof["bound"], "achieved": round(achieved, 2), "peak": peak, "unit": roof["unit"],
                 "frac": round(achieved / peak, 4), "traffic": traffic, "traffic_source": traffic_src,
                 "algorithmic": roof["amount"], "kernel": roof["kernel"],
