@@ -167,7 +167,7 @@ def test_int8_packed_docs_cut_by_tok_rows(oracle_mod, cut):
     assert np.abs(got - ref).max() <= ATOL
 
 
-@pytest.mark.parametrize("Lq, d, dtype", [(32, 128, torch.float16), (300, 128, torch.float16),
+@pytest.mark.parametrize("Lq, d, dtype", [(32, 128, torch.float16), (300, 128, torch.float16), (100, 128, torch.float16),
                                           (32, 1024, torch.float16), (20, 96, torch.bfloat16)])
 def test_packed_scores(oracle_mod, Lq, d, dtype):
     B, Ld = 30, 80

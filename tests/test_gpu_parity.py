@@ -94,6 +94,19 @@ def test_query_lengths(oracle_mod, Lq):
     assert_scores(out, ref)
 
 
+@pytest.mark.parametrize("Lq, d, dtype", [(65, 128, torch.float16), (100, 128, torch.bfloat16),
+                                          (128, 128, torch.float16), (64, 256, torch.float16),
+                                          (40, 256, torch.bfloat16)])
+def test_two_docs_per_workgroup(oracle_mod, Lq, d, dtype):
+    """Single queries whose query tile fills 128 VGPRs score docs 2x and 2x+1 in
+    one workgroup: odd B (the last workgroup holds one doc), empty docs on
+    either side of a pair, tile edges."""
+    lengths = [90, 0, 0, 90, 1, 16, 17, 89, 33, 0, 48, 64, 5]
+    out, ref = run_single(oracle_mod, 13, Lq, 90, d, 400 + Lq + d, dtype=dtype, lengths=lengths)
+    assert_scores(out, ref)
+    assert torch.isneginf(out[1]) and torch.isneginf(out[2]) and torch.isneginf(out[9])
+
+
 @pytest.mark.parametrize("d", [8, 32, 40, 64, 96, 100, 33, 160, 256])
 def test_embedding_dims_stream(oracle_mod, d):
     out, ref = run_single(oracle_mod, 9, 32, 45, d, 130 + d, lengths=[45, 3, 0, 17, 44, 45, 1, 32, 33])
