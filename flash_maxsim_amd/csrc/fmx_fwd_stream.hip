@@ -36,8 +36,13 @@ constexpr int kStreamWaves = 4;
 // the extra bytes in flight gain. fp16/bf16 tiles of 8 k-steps (d > 128) hold
 // 8 KB each: two in flight keep two or more waves per SIMD (four cost d = 192
 // and d = 256 with 64-token queries a quarter of their speed, at one wave).
-template <int KIND, int KS>
-constexpr int stream_depth() { return (KIND != KIND_U8 && KS >= 8) ? 2 : 4; }
+// uint8 passes of a full 128-VGPR query tile (128 rows at d <= 128) also keep
+// two tiles in flight, which with per-tile scale loads fits two waves per
+// SIMD in 256 VGPRs.
+template <int KIND, int NQB, int KS>
+constexpr int stream_depth() {
+  return (KIND != KIND_U8 && KS >= 8) || (KIND == KIND_U8 && NQB * KS >= 32) ? 2 : 4;
+}
 
 // KMASK: d is not exactly 32*KS, so fragment slots past d must read as zero.
 // VEC: uint8 vector load path (FwdArgs::vec); true for fp16/bf16.
@@ -53,16 +58,18 @@ constexpr int stream_depth() { return (KIND != KIND_U8 && KS >= 8) ? 2 : 4; }
 // Waves per SIMD asked of the compiler: three for the one-doc uint8 instance
 // of 64 query rows (the passes of longer queries; 188 VGPRs allowed two, and
 // fitting 168 costs one spill: Lq = 128 139 -> 125 us). The two-doc instance
-// would spill 9 registers in its loop at that budget (75 -> 116 us).
+// would spill 9 registers in its loop at that budget (75 -> 116 us). Two for
+// the uint8 instances of a full 128-VGPR query tile (see stream_depth).
 template <int KIND, int NQB, int KS, bool VEC, int DOCS>
 constexpr int stream_min_waves() {
-  return (KIND == KIND_U8 && VEC && NQB == 4 && KS == 4 && DOCS == 1) ? 3 : 1;
+  if (KIND == KIND_U8 && VEC && NQB == 4 && KS == 4 && DOCS == 1) return 3;
+  return (KIND == KIND_U8 && NQB * KS >= 32) ? 2 : 1;
 }
 
 template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX, bool VEC, int DOCS = 1, bool JOINT = false>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(stream_min_waves<KIND, NQB, KS, VEC, DOCS>())))
 stream_fwd_kernel(FwdArgs a) {
-  constexpr int NW = kStreamWaves, P = stream_depth<KIND, KS>(), QROWS = NQB * 16;
+  constexpr int NW = kStreamWaves, P = stream_depth<KIND, NQB, KS>(), QROWS = NQB * 16;
   constexpr int ESZ = KindInfo<KIND>::esz;
   constexpr bool BF = KindInfo<KIND>::bf;
   constexpr bool U8 = KIND == KIND_U8;
@@ -178,9 +185,9 @@ stream_fwd_kernel(FwdArgs a) {
   // Sequence position -> (doc, tile of that doc); uniform over the wave.
   // Positions past the sequence read an empty range (zeros, no memory access).
   constexpr bool FIXED = !ARGMAX;  // fixed refill pattern (below)
-  constexpr bool GSM = U8 && VEC;  // group scale loads (below)
+  constexpr bool GSM = U8 && VEC && P == 4;  // group scale loads (below)
   static_assert(!GSM || P == 4, "group scale loads map 16 lanes per tile slot");
-  static_assert(!JOINT || (GSM && DOCS == 2), "a joint scale range serves two-doc group loads");
+  static_assert(!JOINT || DOCS == 2, "a joint scale range serves two-doc group loads");
   const rsrc_t nul = make_rsrc(a.D, 0u);
   auto seq_load = [&](Tile<KIND, KS>& T, int sq) {
     const bool past = sq >= ntiles;
@@ -469,8 +476,9 @@ hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
       // One scale range per pair when its offsets stay below 2^31 bytes: a
       // pair of padded scale rows, or the whole packed scale array.
       const int64_t sm_rows = a.tok_group ? a.tok_rows : a.sm_b + a.Ld;
-      if (VEC && sm_rows * 2 + 64 < ((int64_t)1 << 31)) {
-        hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2, VEC>), grid, dim3(256), 0, s, a);
+      constexpr bool GROUPS = VEC && stream_depth<KIND, NQB, KS>() == 4;  // group scale loads
+      if (GROUPS && sm_rows * 2 + 64 < ((int64_t)1 << 31)) {
+        hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2, GROUPS>), grid, dim3(256), 0, s, a);
       } else {
         hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2>), grid, dim3(256), 0, s, a);
       }
@@ -551,13 +559,15 @@ int stream_fwd_ks(int d) {
 }
 
 // Query tokens per pass: as many 16-token blocks as Lq needs, capped so the
-// query tile stays within 128 VGPRs (NQB * KS <= 32), or 64 for uint8 docs,
-// whose ring and dequant registers would otherwise leave one wave per SIMD
-// (two passes of 64 query rows, their doc read once through the XCD's L2,
-// beat one of 128: Lq = 128 over 5000 docs of 512 tokens, 150 -> 132 us).
+// query tile stays within 128 VGPRs (NQB * KS <= 32). uint8 docs take the
+// full tile too since their 128-row instance keeps two waves per SIMD (see
+// stream_depth): one pass instead of two of 64 rows, whose second pass read
+// the doc from L2 but repeated the code widening and affine epilogue (Lq =
+// 128 over 5000 docs of 512 tokens: 121 -> 106 us; Lq = 96: 115 -> 101 us).
 int stream_fwd_nqb(int Lq, int d, bool u8) {
   const int need = (Lq + 15) / 16;
-  const int cap = (u8 ? 16 : 32) / stream_fwd_ks(d);
+  (void)u8;
+  const int cap = 32 / stream_fwd_ks(d);
   const int nqb = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
   return nqb < cap ? nqb : cap;
 }

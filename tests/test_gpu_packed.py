@@ -91,7 +91,7 @@ def test_quantize_packed_layout(oracle_mod, d):
         assert not codes[pad].any() and not sb[pad].any() and not mb[pad].any()
 
 
-@pytest.mark.parametrize("Lq, d", [(32, 128), (7, 64), (200, 128), (32, 100), (16, 512)])
+@pytest.mark.parametrize("Lq, d", [(32, 128), (7, 64), (200, 128), (32, 100), (16, 512), (100, 128)])
 def test_int8_packed_scores(oracle_mod, Lq, d):
     B, Ld = 40, 90
     Q = sim((Lq, d), 60 + Lq)

@@ -274,6 +274,16 @@ def test_int8_doc_pairs(oracle_mod, lengths):
     assert_scores(out, ref)
 
 
+@pytest.mark.parametrize("Lq, d", [(65, 128), (100, 128), (128, 128), (100, 120), (129, 128)])
+def test_int8_full_query_tile(oracle_mod, Lq, d):
+    """uint8 queries of 65-128 tokens at d <= 128 run one 128-row pass, two
+    docs per workgroup with a two-tile ring (d = 120: the generic load
+    instance); 129 tokens run two such passes."""
+    lengths = [512, 0, 16, 15, 0, 0, 300, 511, 64, 65, 2]
+    out, ref, _ = run_int8(oracle_mod, len(lengths), Lq, 512, d, 370 + Lq + d, lengths=lengths)
+    assert_scores(out, ref)
+
+
 def test_int8_unaligned_scale_rows(oracle_mod):
     """Ld % 4 != 0 makes the kernel read scales one token at a time."""
     out, ref, _ = run_int8(oracle_mod, 7, 32, 301, 128, 350, lengths=[301, 300, 299, 1, 0, 150, 17])
