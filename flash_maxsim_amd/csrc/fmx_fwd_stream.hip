@@ -56,10 +56,11 @@ constexpr int stream_depth() {
 // groups start), so the group scale loads (below) take one instruction per
 // array instead of one per doc.
 // Waves per SIMD asked of the compiler: three for the one-doc uint8 instance
-// of 64 query rows (the passes of longer queries; 188 VGPRs allowed two, and
-// fitting 168 costs one spill: Lq = 128 139 -> 125 us). The two-doc instance
-// would spill 9 registers in its loop at that budget (75 -> 116 us). Two for
-// the uint8 instances of a full 128-VGPR query tile (see stream_depth).
+// of 64 query rows (batched or sparse queries of 33-64 tokens; 188 VGPRs
+// allowed two, and fitting 168 costs one spill: measured as the two passes of
+// Lq = 128, 139 -> 125 us). The two-doc instance would spill 9 registers in
+// its loop at that budget (75 -> 116 us). Two for the uint8 instances of a
+// full 128-VGPR query tile (see stream_depth).
 template <int KIND, int NQB, int KS, bool VEC, int DOCS>
 constexpr int stream_min_waves() {
   if (KIND == KIND_U8 && VEC && NQB == 4 && KS == 4 && DOCS == 1) return 3;

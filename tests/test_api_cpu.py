@@ -158,8 +158,8 @@ def test_quantize_and_packed_reject_bad_arguments(lib):
                                  None, 0, None)
     assert rc == FMX_ERR_INVALID and "lengths" in lib.fmx_last_error().decode()
     assert lib.fmx_fwd_packed_workspace_bytes(10, 32, 300, 128) == 0
-    # uint8 docs: 64 query tokens per pass at d = 128, so 200 tokens take 4 passes
-    assert lib.fmx_fwd_int8_packed_workspace_bytes(10, 200, 300, 128) == 4 * 10 * 4
+    # uint8 docs: 128 query tokens per pass at d = 128, so 200 tokens take 2 passes
+    assert lib.fmx_fwd_int8_packed_workspace_bytes(10, 200, 300, 128) == 2 * 10 * 4
 
 
 def test_packed_layout_on_cpu():
