@@ -202,7 +202,9 @@ __global__ void __launch_bounds__(256) quantize_kernel(QuantArgs a) {
           w[i >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(v, i & 3, w[i >> 2]);
         }
         if (a.vec && k0 + 8 <= a.d) {
-          *reinterpret_cast<u32x2_t*>(crow + k0) = u32x2_t{w[0], w[1]};
+          // non-temporal: the codes are read by a later scoring call, not by
+          // this kernel (config 4's docs: 406.6 -> 400.3 us)
+          __builtin_nontemporal_store(u32x2_t{w[0], w[1]}, reinterpret_cast<u32x2_t*>(crow + k0));
         } else {
           for (int i = 0; i < 8 && k0 + i < a.d; ++i) crow[k0 + i] = (uint8_t)(w[i >> 2] >> (8 * (i & 3)));
         }
