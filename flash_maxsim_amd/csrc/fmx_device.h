@@ -65,6 +65,15 @@ __device__ __forceinline__ uint16_t ld2(rsrc_t r, uint32_t voff) {
   return __builtin_amdgcn_raw_buffer_load_b16(r, voff, 0, 0);
 }
 
+// Wave-uniform read of an input that no kernel of the launch writes, through
+// the constant address space: the compiler may then use a scalar load, which
+// counts on lgkmcnt. A vector load of it in a kernel that also stores would
+// be waited for with a vmcnt that also drains the loads issued before it.
+template <typename T>
+__device__ __forceinline__ T ld_uniform(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)p;
+}
+
 // v of lane `src` (0..63), per lane (ds_bpermute: the LDS crossbar, no LDS memory).
 __device__ __forceinline__ uint32_t lane_fetch(uint32_t v, int src) {
   return (uint32_t)__builtin_amdgcn_ds_bpermute(src * 4, (int)v);

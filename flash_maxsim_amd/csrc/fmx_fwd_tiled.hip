@@ -83,6 +83,17 @@ __device__ __forceinline__ void fold_rows(f32x4_t acc, int rowj, int len, bool t
   }
 }
 
+// Workgroup barrier once this wave's LDS accesses have completed, without
+// the workgroup fence of __syncthreads(), which also waits for every vector
+// memory load in flight (vmcnt(0)). The empty asm statements keep the
+// compiler from moving memory accesses across it.
+__device__ __forceinline__ void barrier_lds() {
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt unconstrained
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
+}
+
 template <int KIND, int NW, int NB, int KS, bool KMASK, bool ARGMAX>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
@@ -93,7 +104,15 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
   // chunks, and the argmax instances (whose registers do not fit the twice
   // unrolled tile loop the DMA path needs), stage through VGPRs into
   // 16-byte-padded rows.
-  constexpr bool DMA = !KMASK && !ARGMAX;
+  // The smallest row blocks (16 rows per wave at d <= 128, no argmax) keep
+  // PR = 4 tiles in flight in a register ring instead: their tiles compute in
+  // a fraction of an HBM round trip, and the per-tile barrier of the DMA path
+  // waits for the one tile in flight (Nq = 2 x 32 tokens over 5000 docs:
+  // 92.5 -> 82.2 us). From 32 rows per wave on, the VGPR staging and LDS
+  // stores cost more than the deeper ring gains (Nq = 8 x 32: +3 %).
+  constexpr bool RING = !ARGMAX && NB == 1 && KS == 4;
+  constexpr int PR = 4;
+  constexpr bool DMA = !KMASK && !ARGMAX && !RING;
   constexpr int ROWB = 64 * KS + (DMA ? 0 : 16);  // LDS bytes per token row
   constexpr int BUFB = TJ * ROWB;          // LDS bytes per tile buffer
   constexpr int CPR = 4 * KS;              // 16-byte chunks per token row
@@ -162,21 +181,21 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
     int64_t rows = len;
     const char* base = static_cast<const char*>(a.D);
     if (a.tok_group) {  // packed docs: clamp to the rows of D
-      const int64_t t0 = 4 * a.tok_group[b];
+      const int64_t t0 = 4 * ld_uniform(a.tok_group + b);
       const int64_t avail = t0 < 0 ? 0 : (a.tok_rows > t0 ? a.tok_rows - t0 : 0);
       if (rows > avail) rows = avail;
-      if (avail > 0) base += doc_elem0(a, b) * 2;
+      if (avail > 0) base += t0 * a.sd_l * 2;
     } else {
       base += doc_elem0(a, b) * 2;
     }
     return make_rsrc(base, (uint32_t)rows * rowb);
   };
   auto doc_len = [&](int b) {
-    int l = a.lengths ? a.lengths[b] : a.Ld;
+    int l = a.lengths ? ld_uniform(a.lengths + b) : a.Ld;
     return l < 0 ? 0 : (l > a.Ld ? a.Ld : l);
   };
   u32x4_t stage[CPT];
-  auto load_tile_regs = [&](rsrc_t rd, int t) {
+  auto load_tile_regs = [&](u32x4_t (&dst)[CPT], rsrc_t rd, int t) __attribute__((always_inline)) {
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int chunk = tid + k * NW * 64;
@@ -184,16 +203,19 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
       const int e0 = cc * 8;
       uint32_t off = (uint32_t)(t * TJ + row) * rowb + (uint32_t)(e0 * 2);
       if (KMASK && e0 >= a.d) off = kOOB;
-      stage[k] = ld16(rd, off);
-      if (has_partial && e0 == kp) stage[k] &= prefix_mask16(a.d & 7);
+      dst[k] = ld16(rd, off);
     }
   };
-  auto store_tile_lds = [&](unsigned char* dst) {
+  // The partial 8-wide chunk (d % 8 != 0) is masked here, when the loaded
+  // value is used anyway, so a load is never waited for right after issue.
+  auto store_tile_lds = [&](const u32x4_t (&src)[CPT], unsigned char* dst) __attribute__((always_inline)) {
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int chunk = tid + k * NW * 64;
       const int row = chunk / CPR, cc = chunk - (chunk / CPR) * CPR;
-      *reinterpret_cast<u32x4_t*>(dst + row * ROWB + cc * 16) = stage[k];
+      u32x4_t v = src[k];
+      if (has_partial && cc * 8 == kp) v &= prefix_mask16(a.d & 7);
+      *reinterpret_cast<u32x4_t*>(dst + row * ROWB + cc * 16) = v;
     }
   };
   // DMA: instruction k of wave w fills chunk positions (k*NW + w)*64 .. +63 of
@@ -227,39 +249,11 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
   int len = doc_len(b);
   int nt = len > 0 ? (len + TJ - 1) / TJ : 1;  // an empty doc still takes one fully masked tile
   rsrc_t rd = tile_rsrc(b, len);
-  if constexpr (DMA) {
-    dma_tile(rd, 0, lds0);
-    dma_wait();
-  } else {
-    load_tile_regs(rd, 0);
-    store_tile_lds(ldsa);
-  }
-  __syncthreads();
   int t = 0, par = 0;
-  // One tile: compute from buffer cur while the next tile fills nxt.
-  auto step = [&](unsigned char* const cur, unsigned char* const nxt) __attribute__((always_inline)) -> bool {
-    int nb_doc = b, nt_tile = t + 1, nlen = len;
-    if (nt_tile >= nt) {
-      nb_doc = b + G;
-      nt_tile = 0;
-    }
-    const bool has_next = nb_doc < a.B;
-    rsrc_t rd_next = rd;
-    if (has_next) {
-      if (nb_doc != b) {
-        nlen = doc_len(nb_doc);
-        rd_next = tile_rsrc(nb_doc, nlen);
-      }
-      if constexpr (DMA) {
-        dma_tile(rd_next, nt_tile, nxt);  // nxt was last read before the previous barrier
-      } else {
-        load_tile_regs(rd_next, nt_tile);
-      }
-    }
 
-    // compute tile t of doc b from the current buffer
+  // Tile t of doc b from the LDS tile at base, folded into the running maxima.
+  auto compute_tile = [&](const unsigned char* base) __attribute__((always_inline)) {
     const int j0 = t * TJ;
-    const unsigned char* base = cur;
     if (j0 + TJ <= len) {
       // full tile: branch-free, A-fragments of subtile s+1 read while s computes
       u32x4_t af[2][KS];
@@ -299,71 +293,152 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
         }
       }
     }
-
-    const bool last = t + 1 >= nt;
-    if (last) {
-      // row maxima of doc b -> rowmax[par]
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        float v = m[nb];
-        int ix = mi[nb];
-        if constexpr (ARGMAX) {
-          argmax_over_groups(v, ix);
-        } else {
-          v = max_over_groups(v);
-        }
-        if (g == 0) {
-          rowmax[par][wave * NB * 16 + nb * 16 + c] = v;
-          if constexpr (ARGMAX) rowidx[par][wave * NB * 16 + nb * 16 + c] = ix;
-        }
-        m[nb] = -INFINITY;
-        mi[nb] = 0;
-      }
-    }
-    if constexpr (DMA) {
-      dma_wait();
-    } else {
-      if (has_next) store_tile_lds(nxt);
-    }
-    __syncthreads();
-
-    if (last) {
-      // per-query sums of doc b over this row block
-      for (int64_t qi = qfirst + wave; qi <= qlast; qi += NW) {
-        const int64_t ra = qi * a.Lq > row0 ? qi * a.Lq : row0;
-        const int64_t rz = (qi + 1) * a.Lq < row_end ? (qi + 1) * a.Lq : row_end;
-        float sum = 0.f;
-        for (int64_t r = ra + lane; r < rz; r += 64) {
-          sum += rowmax[par][r - row0];
-          if constexpr (ARGMAX) a.argmax[(qi * a.B + b) * a.Lq + (r - qi * a.Lq)] = rowidx[par][r - row0];
-        }
-        sum = wave_sum(sum);
-        if (lane == 0) {
-          const bool whole = ra == qi * a.Lq && rz == (qi + 1) * a.Lq;
-          if (whole) {
-            a.scores[qi * a.ss_n + (int64_t)b * a.ss_b] = sum;
-          } else {
-            a.partial[(int64_t)rb * a.Nq * a.B + qi * a.B + b] = sum;
-          }
-        }
-      }
-      par ^= 1;
-    }
-    if (!has_next) return false;
-    if (nb_doc != b) {
-      b = nb_doc;
-      len = nlen;
-      nt = len > 0 ? (len + TJ - 1) / TJ : 1;
-      rd = rd_next;
-    }
-    t = nt_tile;
-    return true;
   };
-  if constexpr (DMA) {
+  // At a doc's last tile: its row maxima to rowmax[par], running maxima reset.
+  auto finish_doc = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      float v = m[nb];
+      int ix = mi[nb];
+      if constexpr (ARGMAX) {
+        argmax_over_groups(v, ix);
+      } else {
+        v = max_over_groups(v);
+      }
+      if (g == 0) {
+        rowmax[par][wave * NB * 16 + nb * 16 + c] = v;
+        if constexpr (ARGMAX) rowidx[par][wave * NB * 16 + nb * 16 + c] = ix;
+      }
+      m[nb] = -INFINITY;
+      mi[nb] = 0;
+    }
+  };
+  // After the barrier that follows finish_doc: per-query sums of doc b over
+  // this row block.
+  auto doc_sums = [&]() __attribute__((always_inline)) {
+    for (int64_t qi = qfirst + wave; qi <= qlast; qi += NW) {
+      const int64_t ra = qi * a.Lq > row0 ? qi * a.Lq : row0;
+      const int64_t rz = (qi + 1) * a.Lq < row_end ? (qi + 1) * a.Lq : row_end;
+      float sum = 0.f;
+      for (int64_t r = ra + lane; r < rz; r += 64) {
+        sum += rowmax[par][r - row0];
+        if constexpr (ARGMAX) a.argmax[(qi * a.B + b) * a.Lq + (r - qi * a.Lq)] = rowidx[par][r - row0];
+      }
+      sum = wave_sum(sum);
+      if (lane == 0) {
+        const bool whole = ra == qi * a.Lq && rz == (qi + 1) * a.Lq;
+        if (whole) {
+          a.scores[qi * a.ss_n + (int64_t)b * a.ss_b] = sum;
+        } else {
+          a.partial[(int64_t)rb * a.Nq * a.B + qi * a.B + b] = sum;
+        }
+      }
+    }
+    par ^= 1;
+  };
+
+  if constexpr (RING) {
+    // Register ring: tile j of the walk is loaded into ring slot j % PR, PR
+    // tiles ahead of the tile being computed, and written to LDS buffer j % 2
+    // one step before it is computed. A prefetch cursor (pb, pt) runs ahead
+    // of (b, t); past the end of the walk it loads from an empty range (zeros,
+    // no memory access), so every step issues the same loads and the compiler
+    // waits for exactly the slot it stores. The barrier skips the workgroup
+    // fence of __syncthreads(), whose vmcnt(0) would drain the ring.
+    u32x4_t ring[PR][CPT];
+    int pb = b, pt = 0, pnt = nt;
+    rsrc_t prd = rd;
+    const rsrc_t nul = make_rsrc(a.D, 0u);
+    auto fetch = [&](u32x4_t (&dst)[CPT]) __attribute__((always_inline)) {
+      const bool have = pb < a.B;
+      load_tile_regs(dst, have ? prd : nul, pt);
+      if (!have) return;
+      if (++pt >= pnt) {
+        pb += G;
+        pt = 0;
+        if (pb < a.B) {
+          const int l = doc_len(pb);
+          pnt = l > 0 ? (l + TJ - 1) / TJ : 1;
+          prd = tile_rsrc(pb, l);
+        }
+      }
+    };
+#pragma unroll
+    for (int j = 0; j < PR; ++j) fetch(ring[j]);
+    store_tile_lds(ring[0], ldsa);
+    barrier_lds();
+    // Tile i = (the step's slot S) mod PR: compute it from buffer S % 2, load
+    // tile i + PR into its slot, store tile i + 1 into the other buffer.
+    auto step = [&](auto slot_tag) __attribute__((always_inline)) -> bool {
+      constexpr int S = decltype(slot_tag)::value;
+      fetch(ring[S]);  // slot S held tile i, stored to LDS by the previous step
+      compute_tile(ldsa + (S & 1) * BUFB);
+      const bool last = t + 1 >= nt;
+      if (last) finish_doc();
+      store_tile_lds(ring[(S + 1) % PR], ldsa + ((S + 1) & 1) * BUFB);
+      barrier_lds();
+      if (last) doc_sums();
+      if (last) {
+        b += G;
+        if (b >= a.B) return false;
+        len = doc_len(b);
+        nt = len > 0 ? (len + TJ - 1) / TJ : 1;
+        t = 0;
+      } else {
+        ++t;
+      }
+      return true;
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1 % PR>;
+    using S2 = std::integral_constant<int, 2 % PR>;
+    using S3 = std::integral_constant<int, 3 % PR>;
+    static_assert(PR == 4, "the unrolled walk below names four slots");
+    while (step(S0{}) && step(S1{}) && step(S2{}) && step(S3{})) {
+    }
+  } else if constexpr (DMA) {
+    dma_tile(rd, 0, lds0);
+    dma_wait();
+    __syncthreads();
+    // One tile: compute from buffer cur while the next tile fills nxt.
+    auto step = [&](unsigned char* const cur, unsigned char* const nxt) __attribute__((always_inline)) -> bool {
+      int nb_doc = b, nt_tile = t + 1, nlen = len;
+      if (nt_tile >= nt) {
+        nb_doc = b + G;
+        nt_tile = 0;
+      }
+      const bool has_next = nb_doc < a.B;
+      rsrc_t rd_next = rd;
+      if (has_next) {
+        if (nb_doc != b) {
+          nlen = doc_len(nb_doc);
+          rd_next = tile_rsrc(nb_doc, nlen);
+        }
+        dma_tile(rd_next, nt_tile, nxt);  // nxt was last read before the previous barrier
+      }
+      compute_tile(cur);
+      const bool last = t + 1 >= nt;
+      if (last) finish_doc();
+      dma_wait();
+      __syncthreads();
+      if (last) doc_sums();
+      if (!has_next) return false;
+      if (nb_doc != b) {
+        b = nb_doc;
+        len = nlen;
+        nt = len > 0 ? (len + TJ - 1) / TJ : 1;
+        rd = rd_next;
+      }
+      t = nt_tile;
+      return true;
+    };
     while (step(lds0, lds1) && step(lds1, lds0)) {
     }
   } else {
     // staging path: the tile loop as a plain loop over a run-time buffer index
+    load_tile_regs(stage, rd, 0);
+    store_tile_lds(stage, ldsa);
+    __syncthreads();
     int buf = 0;
     while (true) {
       int nb_doc = b, nt_tile = t + 1, nlen = len;
@@ -378,97 +453,14 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
           nlen = doc_len(nb_doc);
           rd_next = tile_rsrc(nb_doc, nlen);
         }
-        load_tile_regs(rd_next, nt_tile);
+        load_tile_regs(stage, rd_next, nt_tile);
       }
-
-      // compute tile t of doc b from lds[buf]
-      const int j0 = t * TJ;
-      const unsigned char* base = ldsa + buf * BUFB;
-      if (j0 + TJ <= len) {
-        // full tile: branch-free, A-fragments of subtile s+1 read while s computes
-        u32x4_t af[2][KS];
-        read_frags<KS, ROWB, false>(af[0], base, 0, c, g);
-  #pragma unroll
-        for (int s = 0; s < TJ / 16; ++s) {
-          if (s + 1 < TJ / 16) read_frags<KS, ROWB, false>(af[(s + 1) & 1], base, s + 1, c, g);
-          f32x4_t acc[NB];
-          subtile_mfma<BF, NB, KS>(af[s & 1], qf, acc);
-          const int rowj = j0 + s * 16 + 4 * g;
-  #pragma unroll
-          for (int nb = 0; nb < NB; ++nb) fold_rows<ARGMAX>(acc[nb], rowj, len, false, m[nb], mi[nb]);
-        }
-      } else {
-        // a doc's last, partial tile: its ns subtiles (none for an empty doc)
-        // with the same one-ahead fragment reads, rows past len masked. Each
-        // subtile's MFMAs and fold sit in one block after its branch.
-        // (With the largest row blocks the second fragment buffer does not fit
-        // the register budget; those read each subtile's fragments in turn.)
-        constexpr int AB = NB * KS <= 20 ? 2 : 1;
-        const int ns = len > j0 ? (len - j0 + 15) >> 4 : 0;
-        u32x4_t af[AB][KS];
-        if (AB == 2 && ns > 0) read_frags<KS, ROWB, false>(af[0], base, 0, c, g);
-  #pragma unroll
-        for (int s = 0; s < TJ / 16; ++s) {
-          if (s < ns) {
-            if (AB == 1) {
-              read_frags<KS, ROWB, false>(af[0], base, s, c, g);
-            } else if (s + 1 < ns) {
-              read_frags<KS, ROWB, false>(af[(s + 1) % AB], base, s + 1, c, g);
-            }
-            f32x4_t acc[NB];
-            subtile_mfma<BF, NB, KS>(af[s % AB], qf, acc);
-            const int rowj = j0 + s * 16 + 4 * g;
-  #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) fold_rows<ARGMAX>(acc[nb], rowj, len, true, m[nb], mi[nb]);
-          }
-        }
-      }
-
+      compute_tile(ldsa + buf * BUFB);
       const bool last = t + 1 >= nt;
-      if (last) {
-        // row maxima of doc b -> rowmax[par]
-  #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          float v = m[nb];
-          int ix = mi[nb];
-          if constexpr (ARGMAX) {
-            argmax_over_groups(v, ix);
-          } else {
-            v = max_over_groups(v);
-          }
-          if (g == 0) {
-            rowmax[par][wave * NB * 16 + nb * 16 + c] = v;
-            if constexpr (ARGMAX) rowidx[par][wave * NB * 16 + nb * 16 + c] = ix;
-          }
-          m[nb] = -INFINITY;
-          mi[nb] = 0;
-        }
-      }
-      if (has_next) store_tile_lds(ldsa + (buf ^ 1) * BUFB);
+      if (last) finish_doc();
+      if (has_next) store_tile_lds(stage, ldsa + (buf ^ 1) * BUFB);
       __syncthreads();
-
-      if (last) {
-        // per-query sums of doc b over this row block
-        for (int64_t qi = qfirst + wave; qi <= qlast; qi += NW) {
-          const int64_t ra = qi * a.Lq > row0 ? qi * a.Lq : row0;
-          const int64_t rz = (qi + 1) * a.Lq < row_end ? (qi + 1) * a.Lq : row_end;
-          float sum = 0.f;
-          for (int64_t r = ra + lane; r < rz; r += 64) {
-            sum += rowmax[par][r - row0];
-            if constexpr (ARGMAX) a.argmax[(qi * a.B + b) * a.Lq + (r - qi * a.Lq)] = rowidx[par][r - row0];
-          }
-          sum = wave_sum(sum);
-          if (lane == 0) {
-            const bool whole = ra == qi * a.Lq && rz == (qi + 1) * a.Lq;
-            if (whole) {
-              a.scores[qi * a.ss_n + (int64_t)b * a.ss_b] = sum;
-            } else {
-              a.partial[(int64_t)rb * a.Nq * a.B + qi * a.B + b] = sum;
-            }
-          }
-        }
-        par ^= 1;
-      }
+      if (last) doc_sums();
       if (!has_next) break;
       if (nb_doc != b) {
         b = nb_doc;
