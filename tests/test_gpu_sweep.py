@@ -45,6 +45,8 @@ CASES = [
     (4, 8, 10, 33, 128, torch.float16, True),       # tiled, four 8-token queries
     (2, 150, 7, 60, 128, torch.float16, False),     # stream, per-query docs, two passes on one XCD
     (3, 40, 5, 30, 640, torch.bfloat16, True),      # split-d, three queries of a shared doc on one XCD
+    (3, 32, 9, 140, 100, torch.float16, True),      # tiled register ring, masked width with a partial chunk
+    (2, 40, 13, 200, 120, torch.bfloat16, True),    # tiled register ring, masked width, doc walk past 4 tiles
 ]
 
 
