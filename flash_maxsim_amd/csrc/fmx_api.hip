@@ -343,7 +343,8 @@ extern "C" {
 
 size_t fmx_fwd_topk_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld, int64_t d, int64_t k) {
   (void)Ld;
-  if (B < 1 || Lq < 1 || d < 1 || d > FMX_MAX_D || k < 1) return 0;
+  // the scoring part is needed for any k (k = 0 still scores the docs)
+  if (B < 1 || Lq < 1 || d < 1 || d > FMX_MAX_D || k < 0) return 0;
   return topk_fwd_part(B, Lq, d) + fmx_topk_workspace_bytes(1, B, k);
 }
 

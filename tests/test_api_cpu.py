@@ -113,6 +113,25 @@ def test_workspace_sizes(lib):
     assert lib.fmx_bwd_workspace_bytes(1000, 128, 512, 1024) > 0
 
 
+def test_fwd_topk_arguments_and_workspace(lib):
+    # the scoring part of the workspace is sized for any k, k = 0 included
+    ws0 = lib.fmx_fwd_topk_workspace_bytes(10, 1024, 64, 128, 0)
+    assert ws0 >= lib.fmx_fwd_workspace_bytes(1, 10, 1024, 64, 128) > 0
+    assert lib.fmx_fwd_topk_workspace_bytes(10, 1024, 64, 128, 5) >= ws0
+    assert lib.fmx_fwd_topk_workspace_bytes(5000, 32, 300, 128, 100) == 0  # one pass, one chunk
+
+    def call(B, Lq, k, ws, nbytes):
+        return lib.fmx_fwd_topk(0, FAKE, 128, FAKE, 300 * 128, 128, None, B, Lq, 300, 128, k, FAKE, FAKE, FAKE,
+                                ws, nbytes, None)
+
+    assert call(10, 32, 11, None, 0) == FMX_ERR_INVALID
+    assert "exceeds the 10 scores" in lib.fmx_last_error().decode()
+    assert call(2000, 32, 1025, None, 0) == FMX_ERR_UNSUPPORTED
+    assert call(10, 1024, 3, None, 0) == FMX_ERR_WORKSPACE
+    assert call(10, 1024, 3, FAKE + 16, 1 << 20) == FMX_ERR_INVALID
+    assert "256-byte aligned" in lib.fmx_last_error().decode()
+
+
 def test_int8_and_bwd_reject_bad_arguments(lib):
     rc = lib.fmx_fwd_int8(FAKE, 128, FAKE, 300 * 128, 128, FAKE + 1, FAKE, 300, None, FAKE,
                           10, 32, 300, 128, None, 0, None)
