@@ -25,6 +25,8 @@ Configs (the driver's line is the default, c1):
   copy       a device copy of 384 MB, to calibrate HBM byte counters
 --rotate R (R >= 2) cycles R copies of the doc tensor(s) for any config.
 --doc-align A (c4_packed) starts each packed doc on a multiple of A token rows.
+Any single-query shape: s_Lq_B_Ld_d (fp16 docs) or u8_Lq_B_Ld_d (quantize_int8
+codes of the same random docs), e.g. s_32_5000_1024_128.
 
 roofline: the dominant kernel's algorithmic bytes (or flops) per launch divided
 by its average launch duration, timed with HIP events recorded on the stream
@@ -39,6 +41,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -317,6 +320,40 @@ def build(name: str, rotate: int, doc_align: int = 4) -> Workload:
         cfg = {"workload": f"device copy of {n * 2} bytes (counter calibration)", "bytes": n * 2}
         roof = {"bound": "hbm", "amount": 2 * n * 2, "unit": "GB/s", "kernel": "copy"}
         return Workload(cfg, [lambda: dst.copy_(src)], 1, "copies/s", roof)
+
+    shape = re.fullmatch(r"(s|u8)_(\d+)_(\d+)_(\d+)_(\d+)", name)
+    if shape:  # any single-query shape: s_Lq_B_Ld_d (fp16) or u8_Lq_B_Ld_d (uint8 codes)
+        kind = shape.group(1)
+        Lq, B, Ld, d = map(int, shape.groups()[1:])
+        Q = sim((Lq, d), 61, f16)
+        Qd, Qc = Q.to(dev), Q.float()
+        n = min(B, 200)
+        if kind == "s":
+            Dh = sim((B, Ld, d), 62, f16)
+            Ds = _copies(Dh.to(dev), rotate)
+            steps = [lambda D=D: fm.flash_maxsim(Qd, D) for D in Ds]
+            Dc = Dh[:n].float()
+            cpu = lambda: fm.maxsim_naive(Qc, Dc)  # noqa: E731
+            amount, flops = B * Ld * d * 2 + Lq * d * 2 + B * 4, 2 * Lq * B * Ld * d
+            what = "fp16"
+        else:
+            sets = []
+            for _ in range(max(1, rotate)):
+                x = sim((B, Ld, d), 62 + len(sets), torch.float32, dev)
+                sets.append(fm.quantize_int8(x))
+                del x
+            steps = [lambda st=st: fm.flash_maxsim_int8(Qd, *st) for st in sets]
+            cc, cs, cm = (t[:n].cpu() for t in sets[0])
+            cpu = lambda: fm.maxsim_naive(Qc, fm.dequantize_int8(cc, cs, cm))  # noqa: E731
+            amount, flops = B * Ld * (d + 4) + Lq * d * 2 + B * 4, 2 * Lq * B * Ld * d
+            what = "u8"
+        cfg = {"workload": f"single-query Q[{Lq},{d}] x D[{B},{Ld},{d}] {what}", "B": B, "Lq": Lq, "Ld": Ld, "d": d}
+        if rotate > 1:
+            cfg["rotated_doc_copies"] = len(steps)
+        mfma = flops / MFMA_F16_PEAK_TFLOPS / 1e12 > amount / HBM_PEAK_GBS / 1e9
+        roof = ({"bound": "mfma", "amount": flops, "unit": "TFLOP/s", "kernel": "forward"} if mfma else
+                {"bound": "hbm", "amount": amount, "unit": "GB/s", "kernel": "forward"})
+        return Workload(cfg, steps, B, "docs/s", roof, cpu, n, f"maxsim_naive fp32 over the first {n} docs")
 
     raise SystemExit(f"unknown config {name}")
 
