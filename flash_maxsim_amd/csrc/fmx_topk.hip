@@ -17,9 +17,9 @@
 // keys still needed. Keys are distinct, so the selected set is exactly the
 // keys whose leading bits are >= the final prefix. A block scan compacts them
 // into LDS. Intermediate levels write the chunk's k keys (unordered); the last
-// level ranks them by counting (rank = keys greater than it) and writes values
-// and indices best first. Rows longer than C run several levels, each C / k
-// times shorter.
+// level ranks them by counting (rank = keys greater than it; up to 1024 keys)
+// or sorts them (bitonic, in LDS; k up to 8192) and writes values and indices
+// best first. Rows longer than C run several levels, each C / k times shorter.
 #include "fmx_device.h"
 #include "fmx_kernels.h"
 
@@ -39,7 +39,8 @@ __device__ __forceinline__ uint32_t ord_of(float f) {
 }
 
 constexpr int kTopkThreads = 1024;
-constexpr int kTopkMaxK = 1024;                  // FMX_MAX_TOPK
+constexpr int kTopkMaxK = 8192;                  // FMX_MAX_TOPK
+constexpr int kTopkCountK = 1024;                // ranked by counting up to this many keys
 constexpr int kTopkC = kTopkThreads * 16;       // keys per chunk (16 per thread)
 
 template <int CTRL, int ROW_MASK>
@@ -195,13 +196,15 @@ __device__ __forceinline__ void rank_and_write(const uint64_t* sel, int nsel, in
 // indices [c*C, c*C + C) of scores[r, :n]. Otherwise keys_in[r, :n] (0 = no key).
 // Output: the chunk's k best keys to keys_out[r, c*k ...] (0-padded when the
 // chunk holds fewer), or, at the last level, values and indices, best first.
-template <int kTopkE>  // keys per thread: the chunk is 1024 * kTopkE keys
+// kTopkE: keys per thread (the chunk is 1024 * kTopkE keys); MAXK: capacity of
+// the selection buffer, kTopkCountK or kTopkMaxK (k above kTopkCountK).
+template <int kTopkE, int MAXK>
 __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* scores, int64_t s_stride,
                                                                  const uint64_t* keys_in, int64_t n, int k,
                                                                  uint64_t* keys_out, float* values,
                                                                  int64_t* indices, int64_t o_stride) {
   __shared__ uint32_t hist[256];
-  __shared__ __attribute__((aligned(16))) uint64_t sel[kTopkMaxK];
+  __shared__ __attribute__((aligned(16))) uint64_t sel[MAXK];
   __shared__ int wave_tot[kTopkThreads / 64];
   __shared__ uint64_t wmin[kTopkThreads / 64], wmax[kTopkThreads / 64];
   __shared__ int bcast[4];
@@ -253,7 +256,7 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* s
     for (int e = 0; e < kTopkE; ++e) c += key[e] != 0 && (uint32_t)(key[e] >> 32) >= tau;
     int pos = block_exclusive_scan(c, wave_tot, &bcast[3]);
     const int nc = bcast[3];
-    if (nc <= kTopkMaxK) {  // uniform
+    if (nc <= kTopkCountK) {  // uniform
 #pragma unroll
       for (int e = 0; e < kTopkE; ++e)
         if (key[e] != 0 && (uint32_t)(key[e] >> 32) >= tau) sel[pos++] = key[e];
@@ -391,22 +394,56 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* s
   for (int e = 0; e < kTopkE; ++e) {
     const uint64_t kv = key[e];
     if (kv != 0 && want > 0 && (shift == 64 ? true : (kv >> shift) >= prefix)) {
-      if (pos < kTopkMaxK) sel[pos] = kv;
+      if (pos < MAXK) sel[pos] = kv;
       ++pos;
     }
   }
   if (nsel > want) nsel = want;  // exactly `want` by construction; never past sel
   __syncthreads();
 
-  if (values) {
+  if (values && (MAXK <= kTopkCountK || nsel <= kTopkCountK)) {
     rank_and_write(sel, nsel, k, scores + row * s_stride, values + row * o_stride, indices + row * o_stride,
                    nullptr);
+  } else if (values) {
+    // More keys than ranking by counting handles in time (O(n^2)): a bitonic
+    // sort of the selection, descending, padded with 0 keys (which sort last)
+    // to a power of two, then the best k in order.
+    if constexpr (MAXK > kTopkCountK) {
+      int np = 1;
+      while (np < nsel) np <<= 1;
+      for (int t = nsel + tid; t < np; t += kTopkThreads) sel[t] = 0;
+      __syncthreads();
+      for (int size = 2; size <= np; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+          for (int i = tid; i < np / 2; i += kTopkThreads) {
+            const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
+            const bool desc = (lo & size) == 0;  // every merge of the last size is descending
+            const uint64_t x = sel[lo], y = sel[hi];
+            if ((x < y) == desc) {
+              sel[lo] = y;
+              sel[hi] = x;
+            }
+          }
+          __syncthreads();
+        }
+      }
+      const float* scores_row = scores + row * s_stride;
+      for (int t = tid; t < nsel && t < k; t += kTopkThreads) {
+        const uint64_t kv = sel[t];
+        const int64_t idx = (int64_t)(uint32_t)~(uint32_t)kv;
+        float v = float_of((uint32_t)(kv >> 32));
+        if (v == 0.f || v != v) v = scores_row[idx];  // as rank_and_write
+        values[row * o_stride + t] = v;
+        indices[row * o_stride + t] = idx;
+      }
+    }
   } else {
     for (int t = tid; t < k; t += kTopkThreads)
       keys_out[row * nout + (int64_t)blockIdx.x * k + t] = t < nsel ? sel[t] : 0;
   }
 }
 
+template <int MAXK>
 hipError_t run_levels(const TopkArgs& a, hipStream_t s) {
   int64_t n = a.B;
   const uint64_t* in = nullptr;
@@ -418,8 +455,8 @@ hipError_t run_levels(const TopkArgs& a, hipStream_t s) {
     if (chunks > 0x7fffffff || a.Nq > 65535) return hipErrorInvalidValue;
     uint64_t* out = last ? nullptr : bufs[which];
     // a single chunk holds no more keys per thread than the row needs
-    auto kern = n <= 4 * kTopkThreads ? topk_level_kernel<4>
-              : n <= 8 * kTopkThreads ? topk_level_kernel<8> : topk_level_kernel<16>;
+    auto kern = n <= 4 * kTopkThreads ? topk_level_kernel<4, MAXK>
+              : n <= 8 * kTopkThreads ? topk_level_kernel<8, MAXK> : topk_level_kernel<16, MAXK>;
     hipLaunchKernelGGL(kern, dim3((unsigned)chunks, (unsigned)a.Nq), dim3(kTopkThreads), 0, s, a.scores,
                        a.s_stride, in, n, a.k, out, last ? a.values : nullptr, last ? a.indices : nullptr,
                        a.o_stride);
@@ -446,6 +483,9 @@ int64_t topk_ws_keys(int64_t Nq, int64_t B, int64_t k, int64_t C) {
   return 2 * Nq * chunks * k;
 }
 
-hipError_t launch_topk(const TopkArgs& a, hipStream_t s) { return run_levels(a, s); }
+// k up to kTopkCountK keeps the 8 KB selection buffer; larger k the 64 KB one.
+hipError_t launch_topk(const TopkArgs& a, hipStream_t s) {
+  return a.k <= kTopkCountK ? run_levels<kTopkCountK>(a, s) : run_levels<kTopkMaxK>(a, s);
+}
 
 }  // namespace fmx

@@ -6,7 +6,7 @@ and that selection in libflashmaxsim's kernels, back to back on the current
 stream. Extension of the reference API (no counterpart in flash_maxsim 0.1.0).
 
 Ranking: score descending, NaN before every number (as torch.topk ranks NaN),
-equal scores by the smaller doc index; k <= min(B, 1024). Values equal
+equal scores by the smaller doc index; k <= min(B, 8192). Values equal
 torch.topk(scores, k).values; indices are torch.topk's up to the tie order,
 which is fixed here (smaller index first).
 """

@@ -42,7 +42,7 @@ extern "C" {
 #define FMX_DTYPE_F32 2 /* fmx_quantize_int8 sources only */
 
 #define FMX_MAX_D 4096
-#define FMX_MAX_TOPK 1024
+#define FMX_MAX_TOPK 8192
 #define FMX_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20) /* per GPU, see fmx_fwd_noalloc */
 
 /* Library version string ("0.1.0+mi355x"). */

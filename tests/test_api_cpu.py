@@ -126,7 +126,7 @@ def test_fwd_topk_arguments_and_workspace(lib):
 
     assert call(10, 32, 11, None, 0) == FMX_ERR_INVALID
     assert "exceeds the 10 scores" in lib.fmx_last_error().decode()
-    assert call(2000, 32, 1025, None, 0) == FMX_ERR_UNSUPPORTED
+    assert call(9000, 32, 8193, None, 0) == FMX_ERR_UNSUPPORTED  # FMX_MAX_TOPK = 8192
     assert call(10, 1024, 3, None, 0) == FMX_ERR_WORKSPACE
     assert call(10, 1024, 3, FAKE + 16, 1 << 20) == FMX_ERR_INVALID
     assert "256-byte aligned" in lib.fmx_last_error().decode()

@@ -41,6 +41,8 @@ def assert_same_selection(got, want):
 @pytest.mark.parametrize("Nq, B, k", [
     (1, 1, 1), (1, 10, 10), (1, 2048, 100), (1, 2049, 100), (3, 5000, 10), (2, 5000, 512),
     (2, 5000, 513), (1, 4097, 1024), (4, 100000, 64), (1, 300000, 1000), (100, 5000, 100),
+    # k above 1024: bitonic sort of the selection; full sorts; several levels
+    (2, 5000, 1025), (1, 8192, 8192), (3, 3000, 3000), (2, 40000, 5000), (1, 100000, 8192),
 ])
 def test_topk_matches_oracle(oracle_mod, Nq, B, k):
     s = scores_with_ties(B + k, (Nq, B))
@@ -117,6 +119,7 @@ def _topk_inputs(B, Lq, d, dtype, seed):
     (3000, 700, 32, 128, torch.float16),   # large k
     (2000, 30, 65, 256, torch.float16),    # two streaming passes (workspace)
     (1000, 40, 200, 128, torch.float16),   # tiled kernel
+    (5000, 3000, 32, 128, torch.float16),  # k above 1024
 ])
 def test_one_call_topk_equals_selection_of_scores(oracle_mod, B, k, Lq, d, dtype):
     """flash_maxsim_topk (fmx_fwd_topk) returns exactly the oracle's selection
