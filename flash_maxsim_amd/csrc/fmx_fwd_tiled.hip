@@ -36,8 +36,13 @@
 namespace fmx {
 namespace {
 
-constexpr int kTiledNW = 8;                  // waves per workgroup (one workgroup per CU,
-constexpr int kTiledWPC = 8 / kTiledNW;      // two waves per SIMD)
+constexpr int kTiledNW = 8;                  // waves per workgroup
+// Workgroups per CU: one (two waves per SIMD), or two (four waves per SIMD) for
+// row blocks of up to 32 rows per wave at d <= 128, whose registers fit 128
+// VGPRs: their per-tile work is short next to the waits on their tile loads,
+// which a second workgroup hides (Nq = 8 x 32 tokens over 5000 docs 112.6 ->
+// 99.7 us, a 200-token query 108.5 -> 94.8 us).
+constexpr int tiled_wpc(int nb, int ks) { return (ks == 4 && nb <= 2) ? 2 : 1; }
 constexpr int kTileTokens = 64;
 
 // A-fragments of 16-token subtile s from an LDS tile with ROWB-byte rows.
@@ -95,7 +100,8 @@ __device__ __forceinline__ void barrier_lds() {
 }
 
 template <int KIND, int NW, int NB, int KS, bool KMASK, bool ARGMAX>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ void __launch_bounds__(NW * 64)
+__attribute__((amdgpu_waves_per_eu(2 * tiled_wpc(NB, KS), 2 * tiled_wpc(NB, KS))))
 tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
   constexpr int TJ = kTileTokens;
   // Scores of exact-width rows (no k masking, no argmax) stream global -> LDS
@@ -547,7 +553,7 @@ bool tiled_fwd_applicable(int64_t Nq, int64_t Lq, int d) {
 }
 
 // Picks rows per wave (NB) and doc groups (G). `slots` workgroups run at once
-// (kTiledWPC per CU, two waves per SIMD). The slowest workgroup's time is
+// (tiled_wpc per CU). The slowest workgroup's time is
 // about docs-per-group x (rows-per-block + R0): MFMA work per row plus a
 // per-doc streaming cost worth R0 = 545 rows (fitted: 256 query rows over
 // 5000 docs of 300 tokens take 118, 152, 195 and 231 us with 256-, 512-, 768-
@@ -567,8 +573,6 @@ TiledPlan tiled_fwd_plan(int64_t Nq, int64_t B, int64_t Lq, int d, int cus) {
   const int nbs4[kNB] = {8, 6, 5, 4, 3, 2, 1}, nbs8[kNB] = {4, 3, 2, 1, 1, 1, 1};
   const int* nbs = ks == 4 ? nbs4 : nbs8;
   constexpr double kR0 = 545.0;
-  const int slots = (cus > 0 ? cus : 256) * kTiledWPC;
-  const int per_xcd = slots / 8;
   const int64_t rows = Nq * Lq;
   double best_cost = 0;
   bool have = false;
@@ -578,6 +582,8 @@ TiledPlan tiled_fwd_plan(int64_t Nq, int64_t B, int64_t Lq, int d, int cus) {
       p.ks = ks;
       p.nb = nbs[i];
       p.rows_per_block = kTiledNW * 16 * p.nb;
+      const int slots = (cus > 0 ? cus : 256) * tiled_wpc(p.nb, ks);
+      const int per_xcd = slots / 8;
       p.nRB = (int)((rows + p.rows_per_block - 1) / p.rows_per_block);
       int G;
       if (xcd) {
@@ -594,8 +600,9 @@ TiledPlan tiled_fwd_plan(int64_t Nq, int64_t B, int64_t Lq, int d, int cus) {
       p.xcd_map = xcd;
       p.G = G;
       const double rounds = (double)(((int64_t)p.grid + slots - 1) / slots);
-      const double cost =
-          (double)((B + G - 1) / G) * ((double)p.rows_per_block + kR0) * rounds * (xcd ? 1.0 : 1.04);
+      // workgroups sharing a CU share its MFMA rate: a row costs wpc times as much
+      const double cost = (double)((B + G - 1) / G) * ((double)p.rows_per_block * tiled_wpc(p.nb, ks) + kR0) *
+                          rounds * (xcd ? 1.0 : 1.04);
       if (!have || cost < best_cost) {
         best = p;
         best_cost = cost;
