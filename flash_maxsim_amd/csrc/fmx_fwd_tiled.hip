@@ -5,8 +5,8 @@
 // batched scoring (flash_maxsim.py:233-250, config 3), where the reference
 // re-streams every doc once per (query, 16..128-token block).
 //
-// The Nq*Lq query rows are flattened and cut into row blocks of 8 waves x
-// 16*NB rows. A persistent workgroup of eight waves keeps its row block in
+// The Nq*Lq query rows are flattened and cut into row blocks of NW waves x
+// 16*NB rows. A persistent workgroup of NW waves keeps its row block in
 // VGPRs as MFMA B-fragments and walks a fixed set of docs (doc group g: docs
 // g, g+G, g+2G, ...). Each doc streams in 64-token tiles: global -> VGPR
 // staging -> LDS (double-buffered, rows padded by 16 bytes so the 16 rows of a
@@ -42,7 +42,13 @@ constexpr int kTiledNW = 8;                  // waves per workgroup
 // VGPRs: their per-tile work is short next to the waits on their tile loads,
 // which a second workgroup hides (Nq = 8 x 32 tokens over 5000 docs 112.6 ->
 // 99.7 us, a 200-token query 108.5 -> 94.8 us).
-constexpr int tiled_wpc(int nb, int ks) { return (ks == 4 && nb <= 2) ? 2 : 1; }
+// Four-wave workgroups (NW = 4) run three to a CU (three waves per SIMD, 168
+// VGPRs) with 48 or 64 rows per wave at d <= 128: 192- and 256-row blocks
+// with twelve waves per CU where an eight-wave workgroup has eight (Nq = 8 x
+// 32 over 5000 docs 100.1 -> 92.7 us, Nq = 16 x 32 171.1 -> 163.9 us).
+constexpr int tiled_wpc(int nw, int nb, int ks) { return nw == 4 ? 3 : (ks == 4 && nb <= 2) ? 2 : 1; }
+// waves per SIMD: a CU holds wpc workgroups of nw waves over its four SIMDs
+constexpr int tiled_waves_per_simd(int nw, int nb, int ks) { return tiled_wpc(nw, nb, ks) * nw / 4; }
 constexpr int kTileTokens = 64;
 
 // A-fragments of 16-token subtile s from an LDS tile with ROWB-byte rows.
@@ -101,7 +107,7 @@ __device__ __forceinline__ void barrier_lds() {
 
 template <int KIND, int NW, int NB, int KS, bool KMASK, bool ARGMAX>
 __global__ void __launch_bounds__(NW * 64)
-__attribute__((amdgpu_waves_per_eu(2 * tiled_wpc(NB, KS), 2 * tiled_wpc(NB, KS))))
+__attribute__((amdgpu_waves_per_eu(tiled_waves_per_simd(NW, NB, KS), tiled_waves_per_simd(NW, NB, KS))))
 tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
   constexpr int TJ = kTileTokens;
   // Scores of exact-width rows (no k masking, no argmax) stream global -> LDS
@@ -517,6 +523,14 @@ hipError_t dispatch_flags(const FwdArgs& a, const TiledPlan& p, bool am, hipStre
 
 template <int KIND>
 hipError_t dispatch(const FwdArgs& a, const TiledPlan& p, bool am, hipStream_t s) {
+  if (p.nw == 4) {
+    if (p.ks != 4) return hipErrorInvalidValue;
+    switch (p.nb) {
+      case 4: return dispatch_flags<KIND, 4, 4, 4>(a, p, am, s);
+      case 3: return dispatch_flags<KIND, 4, 3, 4>(a, p, am, s);
+      default: return hipErrorInvalidValue;
+    }
+  }
   if (p.ks == 4) {
     switch (p.nb) {
       case 8: return dispatch_flags<KIND, kTiledNW, 8, 4>(a, p, am, s);
@@ -552,8 +566,9 @@ bool tiled_fwd_applicable(int64_t Nq, int64_t Lq, int d) {
   return Nq > 1 || Lq > 16 * stream_fwd_nqb(1 << 20, d);
 }
 
-// Picks rows per wave (NB) and doc groups (G). `slots` workgroups run at once
-// (tiled_wpc per CU). The slowest workgroup's time is
+// Picks waves per workgroup (NW), rows per wave (NB) and doc groups (G).
+// `slots` workgroups run at once (tiled_wpc per CU). The slowest workgroup's
+// time is
 // about docs-per-group x (rows-per-block + R0): MFMA work per row plus a
 // per-doc streaming cost worth R0 = 545 rows (fitted: 256 query rows over
 // 5000 docs of 300 tokens take 118, 152, 195 and 231 us with 256-, 512-, 768-
@@ -565,24 +580,33 @@ bool tiled_fwd_applicable(int64_t Nq, int64_t Lq, int d) {
 // XCD (G a multiple of 8, nRB * G / 8 workgroups per XCD), so each doc tile is
 // fetched once per XCD L2; without it the row blocks of a doc meet in the
 // shared last-level cache instead, which is counted as a few percent of extra
-// cost.
+// cost. Workgroups sharing a CU share its MFMA rate, so a row costs wpc times
+// as much. A four-wave workgroup issues a doc tile's loads from half as many
+// waves, and its per-doc cost is R0 = 700 rows (fitted on 256- to 512-row
+// batches over 5000 docs, which it runs 6 % faster, and 300- and 512-row
+// queries over 1000 docs, which it runs 4 to 7 % slower).
 TiledPlan tiled_fwd_plan(int64_t Nq, int64_t B, int64_t Lq, int d, int cus) {
   TiledPlan best = {};
   const int ks = d <= 128 ? 4 : 8;
   constexpr int kNB = 7;
   const int nbs4[kNB] = {8, 6, 5, 4, 3, 2, 1}, nbs8[kNB] = {4, 3, 2, 1, 1, 1, 1};
   const int* nbs = ks == 4 ? nbs4 : nbs8;
-  constexpr double kR0 = 545.0;
+  constexpr double kR0 = 545.0, kR0NW4 = 700.0;
   const int64_t rows = Nq * Lq;
   double best_cost = 0;
   bool have = false;
-  for (int i = 0; i < kNB; ++i) {
+  for (int i = 0; i < kNB + 2; ++i) {
+    // the last two candidates: four-wave workgroups with NB = 4 and 3 (d <= 128)
+    const int nw = i < kNB ? kTiledNW : 4;
+    if (nw == 4 && ks != 4) continue;
     for (int xcd = 1; xcd >= 0; --xcd) {
       TiledPlan p = {};
       p.ks = ks;
-      p.nb = nbs[i];
-      p.rows_per_block = kTiledNW * 16 * p.nb;
-      const int slots = (cus > 0 ? cus : 256) * tiled_wpc(p.nb, ks);
+      p.nw = nw;
+      p.nb = i < kNB ? nbs[i] : (i == kNB ? 4 : 3);
+      p.rows_per_block = nw * 16 * p.nb;
+      const int wpc = tiled_wpc(nw, p.nb, ks);
+      const int slots = (cus > 0 ? cus : 256) * wpc;
       const int per_xcd = slots / 8;
       p.nRB = (int)((rows + p.rows_per_block - 1) / p.rows_per_block);
       int G;
@@ -600,8 +624,7 @@ TiledPlan tiled_fwd_plan(int64_t Nq, int64_t B, int64_t Lq, int d, int cus) {
       p.xcd_map = xcd;
       p.G = G;
       const double rounds = (double)(((int64_t)p.grid + slots - 1) / slots);
-      // workgroups sharing a CU share its MFMA rate: a row costs wpc times as much
-      const double cost = (double)((B + G - 1) / G) * ((double)p.rows_per_block * tiled_wpc(p.nb, ks) + kR0) *
+      const double cost = (double)((B + G - 1) / G) * ((double)p.rows_per_block * wpc + (nw == 4 ? kR0NW4 : kR0)) *
                           rounds * (xcd ? 1.0 : 1.04);
       if (!have || cost < best_cost) {
         best = p;

@@ -71,13 +71,14 @@ int splitd_fwd_nqb(int Lq, int d);    // 16-token query blocks per pass
 int splitd_fwd_passes(int Lq, int d); // > 1: partial sums in FwdArgs::partial
 hipError_t launch_splitd_fwd(int kind, const FwdArgs& a, bool with_argmax, hipStream_t s);
 
-// Tiled kernel (MFMA-bound regime): persistent 8-wave workgroups keep a block
-// of query rows in VGPRs and stream shared docs through LDS. d <= 256 and at
-// least 256 query rows in total.
+// Tiled kernel (MFMA-bound regime): persistent 8- or 4-wave workgroups keep a
+// block of query rows in VGPRs and stream shared docs through LDS. d <= 256
+// and at least 256 query rows in total.
 struct TiledPlan {
   int ks;              // 32-wide k-steps (4: d <= 128, 8: d <= 256)
+  int nw;              // waves per workgroup (8, or 4 with three workgroups per CU)
   int nb;              // 16-row query blocks per wave
-  int rows_per_block;  // 8 * 16 * nb
+  int rows_per_block;  // nw * 16 * nb
   int nRB;             // row blocks over the Nq*Lq flattened query rows
   int G;               // doc groups (workgroups per row block)
   int xcd_map;         // XCD-aware blockIdx mapping (G % 8 == 0)

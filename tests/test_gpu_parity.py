@@ -445,3 +445,39 @@ def test_tiled_bf16_and_argmax(oracle_mod):
     dQ_ref, dD_ref = oracle_mod.bwd(Qn, Dn, am.cpu().numpy(), g.numpy())
     np.testing.assert_allclose(dQ.double().cpu().numpy(), dQ_ref, rtol=1e-2, atol=2e-2)
     np.testing.assert_allclose(dD.double().cpu().numpy(), dD_ref, rtol=1e-2, atol=2e-2)
+
+
+@pytest.mark.parametrize("Nq, Lq, B, Ld, d, dtype", [
+    (8, 32, 1500, 40, 128, torch.float16),    # 256 rows: one 256-row block (NB = 4)
+    (1, 512, 1600, 40, 128, torch.bfloat16),  # one query over two 256-row blocks: partial sums
+    (6, 64, 1600, 30, 128, torch.bfloat16),   # 384 rows: two 192-row blocks (NB = 3)
+    (3, 100, 1600, 40, 96, torch.float16),    # 192-row blocks, masked width, straddling queries
+    (2, 150, 1600, 30, 100, torch.float16),   # masked width with a partial chunk, straddling
+])
+def test_tiled_four_wave_blocks(oracle_mod, Nq, Lq, B, Ld, d, dtype):
+    # Shapes whose plan (256 CUs) picks four-wave workgroups, three per CU.
+    Q = sim((Nq, Lq, d), 950 + Lq, dtype)
+    D = sim((B, Ld, d), 951 + d, dtype)
+    lengths = torch.randint(0, Ld + 5, (B,), generator=torch.Generator().manual_seed(Lq), dtype=torch.int32)
+    out = fm.flash_maxsim_batched(Q.to(DEV), D.to(DEV), lengths.to(DEV))
+    ref = oracle_mod.maxsim(to_np32(Q), to_np32(D), lengths.numpy())
+    assert_scores(out, ref)
+
+
+@pytest.mark.parametrize("Lq, Ld, d, dtype", [
+    (400, 40, 128, torch.bfloat16),  # two 256-row blocks
+    (300, 30, 96, torch.float16),    # two 192-row blocks, masked width
+])
+def test_tiled_four_wave_argmax(oracle_mod, Lq, Ld, d, dtype):
+    B = 1600
+    s, dQ, dD, ref, am_ref, best, Qn, Dn, g = run_train(oracle_mod, B, Lq, Ld, d, 960 + d, dtype)
+    assert_scores(s, ref[0])
+    from flash_maxsim_amd.flash_maxsim import _launch_fwd, _prep
+
+    Q2 = _prep(torch.from_numpy(Qn).to(dtype).to(DEV), dtype)
+    D2 = _prep(torch.from_numpy(Dn).to(dtype).to(DEV), dtype)
+    _, am = _launch_fwd(Q2[None], D2, None, 1, B, Lq, Ld, d, True, True)
+    assert_argmax(am, am_ref, best, Qn, Dn, d)
+    dQ_ref, dD_ref = oracle_mod.bwd(Qn, Dn, am.cpu().numpy(), g.numpy())
+    np.testing.assert_allclose(dQ.double().cpu().numpy(), dQ_ref, rtol=1e-2, atol=2e-2)
+    np.testing.assert_allclose(dD.double().cpu().numpy(), dD_ref, rtol=1e-2, atol=2e-2)
