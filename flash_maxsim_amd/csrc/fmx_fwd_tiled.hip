@@ -64,6 +64,20 @@ __device__ __forceinline__ void read_frags(u32x4_t (&af)[KS], const unsigned cha
   }
 }
 
+// The same for a doc's partial last tile: rows past `last` (the tile's last
+// row inside the doc) read row `last` again. Their scores repeat that row's,
+// which leaves a running maximum unchanged, so the fold needs no mask.
+template <int KS, int ROWB, bool SWZ>
+__device__ __forceinline__ void read_frags_upto(u32x4_t (&af)[KS], const unsigned char* base, int s, int last,
+                                                int c, int g) {
+  const int r = s * 16 + c < last ? s * 16 + c : last;
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) {
+    const int j = kk * 4 + g;
+    af[kk] = *reinterpret_cast<const u32x4_t*>(base + r * ROWB + (SWZ ? (j ^ (r & 15)) : j) * 16);
+  }
+}
+
 // S for one subtile against every query block of the wave; k-step outer so the
 // NB accumulation chains are independent and issue back to back.
 template <bool BF, int NB, int KS>
@@ -281,27 +295,38 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
       }
     } else {
       // a doc's last, partial tile: its ns subtiles (none for an empty doc)
-      // with the same one-ahead fragment reads, rows past len masked. Each
-      // subtile's MFMAs and fold sit in one block after its branch.
+      // with the same one-ahead fragment reads. Rows past len repeat the
+      // doc's last row (scores only: no mask in the fold), or are masked
+      // (argmax, whose index must not move to a repeat). Each subtile's MFMAs
+      // and fold sit in one block after its branch.
       // (With the largest row blocks the second fragment buffer does not fit
       // the register budget; those read each subtile's fragments in turn.)
       constexpr int AB = NB * KS <= 20 ? 2 : 1;
+      constexpr bool REPEAT = !ARGMAX;
       const int ns = len > j0 ? (len - j0 + 15) >> 4 : 0;
+      const int last = len - 1 - j0;
       u32x4_t af[AB][KS];
-      if (AB == 2 && ns > 0) read_frags<KS, ROWB, DMA>(af[0], base, 0, c, g);
+      auto frags = [&](u32x4_t (&dst)[KS], int s) __attribute__((always_inline)) {
+        if constexpr (REPEAT) {
+          read_frags_upto<KS, ROWB, DMA>(dst, base, s, last, c, g);
+        } else {
+          read_frags<KS, ROWB, DMA>(dst, base, s, c, g);
+        }
+      };
+      if (AB == 2 && ns > 0) frags(af[0], 0);
 #pragma unroll
       for (int s = 0; s < TJ / 16; ++s) {
         if (s < ns) {
           if (AB == 1) {
-            read_frags<KS, ROWB, DMA>(af[0], base, s, c, g);
+            frags(af[0], s);
           } else if (s + 1 < ns) {
-            read_frags<KS, ROWB, DMA>(af[(s + 1) % AB], base, s + 1, c, g);
+            frags(af[(s + 1) % AB], s + 1);
           }
           f32x4_t acc[NB];
           subtile_mfma<BF, NB, KS>(af[s % AB], qf, acc);
           const int rowj = j0 + s * 16 + 4 * g;
 #pragma unroll
-          for (int nb = 0; nb < NB; ++nb) fold_rows<ARGMAX>(acc[nb], rowj, len, true, m[nb], mi[nb]);
+          for (int nb = 0; nb < NB; ++nb) fold_rows<ARGMAX>(acc[nb], rowj, len, !REPEAT, m[nb], mi[nb]);
         }
       }
     }
