@@ -297,8 +297,8 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
       // a doc's last, partial tile: its ns subtiles (none for an empty doc)
       // with the same one-ahead fragment reads. Rows past len repeat the
       // doc's last row (scores only: no mask in the fold), or are masked
-      // (argmax, whose index must not move to a repeat). Each subtile's MFMAs
-      // and fold sit in one block after its branch.
+      // (argmax instances). Each subtile's MFMAs and fold sit in one block
+      // after its branch.
       // (With the largest row blocks the second fragment buffer does not fit
       // the register budget; those read each subtile's fragments in turn.)
       constexpr int AB = NB * KS <= 20 ? 2 : 1;
