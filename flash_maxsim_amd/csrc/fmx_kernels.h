@@ -114,7 +114,7 @@ struct TopkArgs {
   const float* scores;        // [Nq, B], row stride s_stride
   int64_t s_stride;
   int64_t Nq, B;
-  int k;                      // 1 <= k <= min(B, 1024)
+  int k;                      // 1 <= k <= min(B, 8192)
   float* values;              // [Nq, k], row stride o_stride
   int64_t* indices;           // [Nq, k], row stride o_stride
   int64_t o_stride;

@@ -186,6 +186,24 @@ def test_packed_scores(oracle_mod, Lq, d, dtype):
     np.testing.assert_array_equal(out.cpu().numpy(), padded.cpu().numpy())
 
 
+def test_packed_four_wave_tiled(oracle_mod):
+    # 400-token query over 1600 packed docs: the tiled plan (256 CUs) picks two
+    # 256-row blocks of four-wave workgroups, three per CU.
+    B, Ld, Lq, d = 1600, 40, 400, 128
+    Q = sim((Lq, d), 90)
+    D = sim((B, Ld, d), 91)
+    lengths = torch.randint(0, Ld + 1, (B,), generator=torch.Generator().manual_seed(92), dtype=torch.int32)
+    packed = fm.pack_docs(D.to(DEV), lengths.to(DEV))
+    out = fm.flash_maxsim_packed(Q.to(DEV), packed)
+    ref = oracle_mod.maxsim(to_np32(Q), to_np32(D), lengths.numpy())[0]
+    got = out.double().cpu().numpy()
+    fin = np.isfinite(ref)
+    np.testing.assert_array_equal(np.isfinite(got), fin)
+    assert np.abs(got[fin] - ref[fin]).max() <= ATOL
+    padded = fm.flash_maxsim(Q.to(DEV), D.to(DEV), lengths.to(DEV))
+    np.testing.assert_array_equal(out.cpu().numpy(), padded.cpu().numpy())
+
+
 def test_packed_empty_and_all_empty(oracle_mod):
     Q = sim((32, 128), 80)
     D = sim((5, 16, 128), 81)
