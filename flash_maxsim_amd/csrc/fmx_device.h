@@ -219,6 +219,26 @@ __device__ __forceinline__ float wave_sum(float v) {
   return lo + hi;
 }
 
+// Sum over each aligned group of lq lanes (lq a power of two up to 64, the
+// same for the whole wave), in every lane of the group: the first log2(lq)
+// steps of wave_sum.
+__device__ __forceinline__ float group_sum(float v, int lq) {
+  if (lq > 1) v += dpp_mov<0xB1>(v);
+  if (lq > 2) v += dpp_mov<0x4E>(v);
+  if (lq > 4) v += dpp_mov<0x141>(v);
+  if (lq > 8) v += dpp_mov<0x140>(v);
+  float lo, hi;
+  if (lq > 16) {
+    halves16(v, lo, hi);
+    v = lo + hi;
+  }
+  if (lq > 32) {
+    halves32(v, lo, hi);
+    v = lo + hi;
+  }
+  return v;
+}
+
 // Running max of a lane's value over the four lanes c, c+16, c+32, c+48 (the
 // four row groups of an MFMA result column), left in every lane.
 __device__ __forceinline__ float max_over_groups(float v) {
