@@ -464,6 +464,26 @@ def test_tiled_four_wave_blocks(oracle_mod, Nq, Lq, B, Ld, d, dtype):
     assert_scores(out, ref)
 
 
+@pytest.mark.parametrize("Nq, Lq, d, dtype", [
+    (300, 1, 128, torch.float16),    # one row per query: no lane exchange
+    (150, 2, 128, torch.bfloat16),
+    (70, 4, 100, torch.float16),     # masked width (VGPR staging)
+    (40, 16, 128, torch.float16),
+    (9, 64, 256, torch.bfloat16),    # d = 256 (8 k-steps), a full 64-row window per query
+    (20, 64, 128, torch.float16),
+])
+def test_tiled_window_sums(oracle_mod, Nq, Lq, d, dtype):
+    # Query lengths dividing 64: each 64-row window of a row block holds whole
+    # queries, summed by one lane-group sum per window.
+    B, Ld = 70, 60
+    Q = sim((Nq, Lq, d), 970 + Lq, dtype)
+    D = sim((B, Ld, d), 971 + d, dtype)
+    lengths = torch.randint(0, Ld + 5, (B,), generator=torch.Generator().manual_seed(Nq), dtype=torch.int32)
+    out = fm.flash_maxsim_batched(Q.to(DEV), D.to(DEV), lengths.to(DEV))
+    ref = oracle_mod.maxsim(to_np32(Q), to_np32(D), lengths.numpy())
+    assert_scores(out, ref)
+
+
 @pytest.mark.parametrize("Lq, Ld, d, dtype", [
     (400, 40, 128, torch.bfloat16),  # two 256-row blocks
     (300, 30, 96, torch.float16),    # two 192-row blocks, masked width
