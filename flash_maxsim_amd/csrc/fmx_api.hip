@@ -39,10 +39,10 @@ struct FwdPlan {
   int passes;
 };
 
-FwdPlan plan_fwd(int64_t Lq, int64_t d, bool u8 = false) {
+FwdPlan plan_fwd(int64_t Lq, int64_t d) {
   FwdPlan p;
   p.splitd = d > 256;
-  p.passes = p.splitd ? fmx::splitd_fwd_passes((int)Lq, (int)d) : fmx::stream_fwd_passes((int)Lq, (int)d, u8);
+  p.passes = p.splitd ? fmx::splitd_fwd_passes((int)Lq, (int)d) : fmx::stream_fwd_passes((int)Lq, (int)d);
   return p;
 }
 
@@ -66,9 +66,9 @@ bool use_tiled(int64_t Nq, int64_t Lq, int64_t d, int shared_docs) {
 
 // Streaming / split-d kernels: per-pass partial sums when the query needs
 // several passes.
-size_t stream_ws_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t d, bool u8 = false) {
+size_t stream_ws_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t d) {
   if (Lq < 1 || d < 1 || d > FMX_MAX_D || Nq < 1 || B < 1) return 0;
-  const FwdPlan p = plan_fwd(Lq, d, u8);
+  const FwdPlan p = plan_fwd(Lq, d);
   return p.passes > 1 ? (size_t)p.passes * (size_t)Nq * (size_t)B * sizeof(float) : 0;
 }
 
@@ -158,7 +158,7 @@ size_t fmx_fwd_workspace_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t Ld, in
 
 size_t fmx_fwd_int8_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld, int64_t d) {
   (void)Ld;
-  return stream_ws_bytes(1, B, Lq, d, true);
+  return stream_ws_bytes(1, B, Lq, d);
 }
 
 }  // extern "C"
@@ -253,7 +253,7 @@ int int8_impl(const void* Q, int64_t q_stride_l, const uint8_t* D, int64_t d_str
     return fail(FMX_ERR_INVALID, "scales and mins must be 2-byte aligned");
   if (!tok_group && sm_stride_b < Ld)
     return fail(FMX_ERR_INVALID, "scale doc stride %lld < Ld", (long long)sm_stride_b);
-  const size_t need = stream_ws_bytes(1, B, Lq, d, true);
+  const size_t need = stream_ws_bytes(1, B, Lq, d);
   if (need > 0 && (!workspace || workspace_bytes < need))
     return fail(FMX_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
 
@@ -387,7 +387,7 @@ int fmx_fwd_packed(int dtype, const void* Q, int64_t q_stride_l, int64_t Lq, con
 }
 
 size_t fmx_fwd_int8_packed_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld_max, int64_t d) {
-  return stream_ws_bytes(1, B, Lq, d, true);
+  return stream_ws_bytes(1, B, Lq, d);
 }
 
 int fmx_fwd_int8_packed(const void* Q, int64_t q_stride_l, int64_t Lq, const uint8_t* codes, int64_t c_stride_l,

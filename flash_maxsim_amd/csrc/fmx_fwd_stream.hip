@@ -522,7 +522,7 @@ hipError_t dispatch_flags(const FwdArgs& a, bool am, hipStream_t s) {
 
 template <int KIND, int KS>
 hipError_t dispatch_nqb(const FwdArgs& a, bool am, hipStream_t s) {
-  const int nqb = stream_fwd_nqb(a.Lq, a.d, KIND == KIND_U8);
+  const int nqb = stream_fwd_nqb(a.Lq, a.d);
   switch (nqb) {
     case 1: return dispatch_flags<KIND, 1, KS>(a, am, s);
     case 2: return dispatch_flags<KIND, 2, KS>(a, am, s);
@@ -565,16 +565,15 @@ int stream_fwd_ks(int d) {
 // stream_depth): one pass instead of two of 64 rows, whose second pass read
 // the doc from L2 but repeated the code widening and affine epilogue (Lq =
 // 128 over 5000 docs of 512 tokens: 121 -> 106 us; Lq = 96: 115 -> 101 us).
-int stream_fwd_nqb(int Lq, int d, bool u8) {
+int stream_fwd_nqb(int Lq, int d) {
   const int need = (Lq + 15) / 16;
-  (void)u8;
   const int cap = 32 / stream_fwd_ks(d);
   const int nqb = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
   return nqb < cap ? nqb : cap;
 }
 
-int stream_fwd_passes(int Lq, int d, bool u8) {
-  const int rows = 16 * stream_fwd_nqb(Lq, d, u8);
+int stream_fwd_passes(int Lq, int d) {
+  const int rows = 16 * stream_fwd_nqb(Lq, d);
   return (Lq + rows - 1) / rows;
 }
 

@@ -59,8 +59,8 @@ struct BwdArgs {
 // straight from HBM into VGPRs): d <= 256.
 bool stream_fwd_supported(int d);
 int stream_fwd_ks(int d);             // 32-wide k-steps held per fragment row
-int stream_fwd_nqb(int Lq, int d, bool u8 = false);    // 16-token query blocks per pass
-int stream_fwd_passes(int Lq, int d, bool u8 = false); // > 1: partial sums in FwdArgs::partial
+int stream_fwd_nqb(int Lq, int d);     // 16-token query blocks per pass (fp16/bf16 and uint8 docs)
+int stream_fwd_passes(int Lq, int d);  // > 1: partial sums in FwdArgs::partial
 hipError_t launch_stream_fwd(int kind, const FwdArgs& a, bool with_argmax, hipStream_t s);
 
 // Split-d kernel: the eight waves of a workgroup each own a slice of d and
