@@ -96,15 +96,31 @@ def test_query_lengths(oracle_mod, Lq):
 
 @pytest.mark.parametrize("Lq, d, dtype", [(65, 128, torch.float16), (100, 128, torch.bfloat16),
                                           (128, 128, torch.float16), (64, 256, torch.float16),
-                                          (40, 256, torch.bfloat16)])
+                                          (40, 256, torch.bfloat16),
+                                          # docs of up to 256 tokens: two per workgroup at any Lq
+                                          (32, 128, torch.float16), (16, 128, torch.bfloat16),
+                                          (1, 128, torch.float16), (48, 128, torch.float16),
+                                          (20, 64, torch.float16), (8, 256, torch.bfloat16)])
 def test_two_docs_per_workgroup(oracle_mod, Lq, d, dtype):
-    """Single queries whose query tile fills 128 VGPRs score docs 2x and 2x+1 in
-    one workgroup: odd B (the last workgroup holds one doc), empty docs on
-    either side of a pair, tile edges."""
+    """Single queries whose query tile fills 128 VGPRs, or docs of up to 256
+    tokens, score docs 2x and 2x+1 in one workgroup: odd B (the last workgroup
+    holds one doc), empty docs on either side of a pair, tile edges."""
     lengths = [90, 0, 0, 90, 1, 16, 17, 89, 33, 0, 48, 64, 5]
     out, ref = run_single(oracle_mod, 13, Lq, 90, d, 400 + Lq + d, dtype=dtype, lengths=lengths)
     assert_scores(out, ref)
     assert torch.isneginf(out[1]) and torch.isneginf(out[2]) and torch.isneginf(out[9])
+
+
+@pytest.mark.parametrize("Ld", [256, 257, 200, 64])
+def test_two_docs_length_boundary(oracle_mod, Ld):
+    # 32-token query: docs of up to 256 tokens pair up in a workgroup, longer
+    # ones (257) take one each; both sides of the boundary, full and ragged
+    # lengths.
+    B = 41
+    lengths = torch.randint(0, Ld + 1, (B,), generator=torch.Generator().manual_seed(Ld), dtype=torch.int32)
+    lengths[:3] = torch.tensor([Ld, 0, Ld - 1])
+    out, ref = run_single(oracle_mod, B, 32, Ld, 128, 450 + Ld, lengths=lengths.numpy())
+    assert_scores(out, ref)
 
 
 @pytest.mark.parametrize("d", [8, 32, 40, 64, 96, 100, 33, 160, 256])
