@@ -486,17 +486,19 @@ hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
       return hipGetLastError();
     }
   }
-  if constexpr (KIND != KIND_U8 && !ARGMAX && NQB * KS >= 4 && !KMASK) {
+  if constexpr (KIND != KIND_U8 && !ARGMAX && NQB * KS >= 4) {
     // fp16/bf16 docs of one query whose query tile fills 128 VGPRs: two docs
     // per workgroup as well (Q[96..128, 128] x 5000 docs of 300 tokens:
-    // 85.6 -> 76.4 and 91.5 -> 79.8 us; 1024-token docs unchanged). Smaller
-    // tiles lose a wave per SIMD to the second doc's registers, which costs
-    // long docs (Lq = 32: 300-token docs +4.5 %, 1024 +2 %) but pays for docs
-    // of up to 256 tokens, whose per-workgroup query load and ring start-up
-    // are then shared by two docs (Lq = 32: 64-token docs 46.8 -> 32.4 us,
-    // 77 tokens 26.7 -> 19.9 us, 160 tokens 60.9 -> 52.6 us; Lq = 16 and 64
-    // over 77-token docs -26 % and -17 %). Masked widths fall to one.
-    if (a.Nq == 1 && npass == 1 && !a.qidx && (NQB * KS >= 32 || a.Ld <= 256)) {
+    // 85.6 -> 76.4 and 91.5 -> 79.8 us; 1024-token docs unchanged); with
+    // masked widths they fall to one (d = 96, Lq = 128: +10 %). Smaller tiles
+    // lose a wave per SIMD to the second doc's registers, which costs long
+    // docs (Lq = 32: 300-token docs +4.5 %, 1024 +2 %) but pays for docs of up
+    // to 256 tokens, whose per-workgroup query load and ring start-up are then
+    // shared by two docs (Lq = 32: 64-token docs 46.8 -> 32.4 us, 77 tokens
+    // 26.7 -> 19.9 us, 160 tokens 60.9 -> 52.6 us; Lq = 16 and 64 over
+    // 77-token docs -26 % and -17 %; d = 96: 77 tokens -30 %, 128 -22 %).
+    constexpr bool BIG = NQB * KS >= 32;
+    if (a.Nq == 1 && npass == 1 && !a.qidx && (BIG ? !KMASK : a.Ld <= 256)) {
       hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2>), dim3((unsigned)((a.B + 1) / 2)),
                          dim3(256), 0, s, a);
       return hipGetLastError();

@@ -100,7 +100,8 @@ def test_query_lengths(oracle_mod, Lq):
                                           # docs of up to 256 tokens: two per workgroup at any Lq
                                           (32, 128, torch.float16), (16, 128, torch.bfloat16),
                                           (1, 128, torch.float16), (48, 128, torch.float16),
-                                          (20, 64, torch.float16), (8, 256, torch.bfloat16)])
+                                          (20, 64, torch.float16), (8, 256, torch.bfloat16),
+                                          (32, 96, torch.float16), (24, 100, torch.bfloat16)])
 def test_two_docs_per_workgroup(oracle_mod, Lq, d, dtype):
     """Single queries whose query tile fills 128 VGPRs, or docs of up to 256
     tokens, score docs 2x and 2x+1 in one workgroup: odd B (the last workgroup
