@@ -60,8 +60,8 @@ int device_cus() {
 }
 
 // Whether fmx_fwd takes the tiled (MFMA-bound) kernel for this call.
-bool use_tiled(int64_t Nq, int64_t Lq, int64_t d, int shared_docs) {
-  return (shared_docs || Nq == 1) && fmx::tiled_fwd_applicable(Nq, Lq, (int)d);
+bool use_tiled(int64_t Nq, int64_t Lq, int64_t Ld, int64_t d, int shared_docs) {
+  return (shared_docs || Nq == 1) && fmx::tiled_fwd_applicable(Nq, Lq, Ld, (int)d);
 }
 
 // Streaming / split-d kernels: per-pass partial sums when the query needs
@@ -75,7 +75,7 @@ size_t stream_ws_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t d) {
 // Upper bound over the kernels fmx_fwd may pick for these sizes.
 size_t fwd_ws_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t d) {
   size_t n = stream_ws_bytes(Nq, B, Lq, d);
-  if (Nq >= 1 && B >= 1 && Lq >= 1 && fmx::tiled_fwd_applicable(Nq, Lq, (int)d)) {
+  if (Nq >= 1 && B >= 1 && Lq >= 1 && fmx::tiled_fwd_possible(Nq, Lq, (int)d)) {
     const fmx::TiledPlan p = fmx::tiled_fwd_plan(Nq, B, Lq, (int)d, device_cus());
     const size_t t = fmx::tiled_fwd_workspace_bytes(p, Nq, B);
     if (t > n) n = t;
@@ -178,7 +178,7 @@ int fwd_impl(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, c
   if (!Q || !D || !scores) return fail(FMX_ERR_INVALID, "Q, D and scores must be non-null");
   if (!aligned16(Q) || !aligned16(D)) return fail(FMX_ERR_INVALID, "Q and D must be 16-byte aligned");
   if (Nq > 1 && (q_stride_n & 7)) return fail(FMX_ERR_INVALID, "Q query stride must be a multiple of 8");
-  const bool tiled = use_tiled(Nq, Lq, d, shared_docs);
+  const bool tiled = use_tiled(Nq, Lq, Ld, d, shared_docs);
   fmx::TiledPlan tp = {};
   size_t need;
   if (tiled) {

@@ -629,10 +629,22 @@ hipError_t dispatch(const FwdArgs& a, const TiledPlan& p, bool am, hipStream_t s
 // query (Nq = 2, Lq = 32: 93 against 103 us; Nq = 4: 96 against 198 us at
 // B = 5000, Ld = 300); a single query comes here once it needs more than one
 // pass of the streaming kernel (Lq = 200: 108 against 164 us), below that
-// the streaming kernel is faster (Lq = 96: 82 against 93 us).
-bool tiled_fwd_applicable(int64_t Nq, int64_t Lq, int d) {
+// the streaming kernel is faster (Lq = 96: 82 against 93 us), except over
+// short docs: the streaming kernel loads its query tile once per workgroup of
+// one or two docs, and from 33 query rows over docs of up to 96 tokens, or 65
+// rows over up to 160, that load outweighs what the persistent tiled
+// workgroups (query tile loaded once) lose elsewhere (d <= 128, 5000 docs:
+// 128 rows over 77-token docs 33.3 -> 25.3 us, at d = 96 45.8 -> 24.8 us; 48
+// and 64 rows over 77 tokens -5 % and -8 %; 96 rows over 150 tokens -7 %; 32
+// rows over 77 tokens and 64 over 150 stay faster streamed).
+bool tiled_fwd_applicable(int64_t Nq, int64_t Lq, int64_t Ld, int d) {
   if (d < 1 || d > 256) return false;
-  return Nq > 1 || Lq > 16 * stream_fwd_nqb(1 << 20, d);
+  if (Nq > 1 || Lq > 16 * stream_fwd_nqb(1 << 20, d)) return true;
+  return d <= 128 && ((Lq > 32 && Ld <= 96) || (Lq > 64 && Ld <= 160));
+}
+
+bool tiled_fwd_possible(int64_t Nq, int64_t Lq, int d) {
+  return d >= 1 && d <= 256 && (Nq > 1 || Lq > 32);
 }
 
 // Picks waves per workgroup (NW), rows per wave (NB) and doc groups (G).

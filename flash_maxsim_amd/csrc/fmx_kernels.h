@@ -85,7 +85,8 @@ struct TiledPlan {
   int grid;            // workgroups launched
   int straddle;        // some query spans two row blocks: partial sums + second pass
 };
-bool tiled_fwd_applicable(int64_t Nq, int64_t Lq, int d);
+bool tiled_fwd_applicable(int64_t Nq, int64_t Lq, int64_t Ld, int d);  // fmx_fwd's choice
+bool tiled_fwd_possible(int64_t Nq, int64_t Lq, int d);                 // for some Ld (workspace bounds)
 TiledPlan tiled_fwd_plan(int64_t Nq, int64_t B, int64_t Lq, int d, int cus);
 size_t tiled_fwd_workspace_bytes(const TiledPlan& p, int64_t Nq, int64_t B);
 hipError_t launch_tiled_fwd(int kind, const FwdArgs& a, const TiledPlan& p, bool with_argmax, hipStream_t s);

@@ -112,6 +112,28 @@ def test_two_docs_per_workgroup(oracle_mod, Lq, d, dtype):
     assert torch.isneginf(out[1]) and torch.isneginf(out[2]) and torch.isneginf(out[9])
 
 
+@pytest.mark.parametrize("Lq, dtype", [(65, torch.float16), (100, torch.bfloat16), (128, torch.float16)])
+def test_two_docs_full_query_tile(oracle_mod, Lq, dtype):
+    # 65-128-row queries over docs longer than 160 tokens stay on the streaming
+    # kernel, two docs per workgroup (shorter docs go to the tiled kernel).
+    lengths = [200, 0, 0, 200, 1, 16, 17, 199, 161, 0, 48, 64, 5]
+    out, ref = run_single(oracle_mod, 13, Lq, 200, 128, 430 + Lq, dtype=dtype, lengths=lengths)
+    assert_scores(out, ref)
+
+
+@pytest.mark.parametrize("Lq, Ld, d", [(33, 96, 128), (64, 97, 128), (65, 160, 128), (128, 60, 96),
+                                       (100, 161, 128), (48, 96, 100)])
+def test_single_query_short_docs(oracle_mod, Lq, Ld, d):
+    # Single queries over short docs: the tiled kernel from 33 rows over docs of
+    # up to 96 tokens and from 65 rows over up to 160; the boundaries' other
+    # sides stay streamed.
+    B = 37
+    lengths = torch.randint(0, Ld + 1, (B,), generator=torch.Generator().manual_seed(Lq + Ld), dtype=torch.int32)
+    lengths[:2] = torch.tensor([Ld, 0])
+    out, ref = run_single(oracle_mod, B, Lq, Ld, d, 460 + Lq, lengths=lengths.numpy())
+    assert_scores(out, ref)
+
+
 @pytest.mark.parametrize("Ld", [256, 257, 200, 64])
 def test_two_docs_length_boundary(oracle_mod, Ld):
     # 32-token query: docs of up to 256 tokens pair up in a workgroup, longer
