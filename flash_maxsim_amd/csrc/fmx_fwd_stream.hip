@@ -97,8 +97,11 @@ stream_fwd_kernel(FwdArgs a) {
   }
   int qi, b;
   if constexpr (DOCS == 2) {
-    qi = 0;
-    b = 2 * xi;
+    // workgroup xi: docs 2p and 2p + 1 of query qi (per-query docs: that
+    // query's own docs, rows qi * B + b)
+    const int pairs = (a.B + 1) / 2;
+    qi = xi / pairs;
+    b = 2 * (xi - qi * pairs);
   } else if (a.shared_docs && a.Nq > 1) {
     // Queries of one doc run back to back so the doc streams from HBM once
     // and the other queries find it in cache.
@@ -498,9 +501,9 @@ hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
     // 26.7 -> 19.9 us, 160 tokens 60.9 -> 52.6 us; Lq = 16 and 64 over
     // 77-token docs -26 % and -17 %; d = 96: 77 tokens -30 %, 128 -22 %).
     constexpr bool BIG = NQB * KS >= 32;
-    if (a.Nq == 1 && npass == 1 && !a.qidx && (BIG ? !KMASK : a.Ld <= 256)) {
-      hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2>), dim3((unsigned)((a.B + 1) / 2)),
-                         dim3(256), 0, s, a);
+    if ((a.Nq == 1 || !a.shared_docs) && npass == 1 && !a.qidx && (BIG ? !KMASK : a.Ld <= 256)) {
+      hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2>),
+                         dim3((unsigned)(a.Nq * ((a.B + 1) / 2))), dim3(256), 0, s, a);
       return hipGetLastError();
     }
   }

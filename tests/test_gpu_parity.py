@@ -225,6 +225,24 @@ def test_batched_varlen_and_not_shared(oracle_mod):
     assert_scores(out, ref)
 
 
+@pytest.mark.parametrize("Nq, Lq, B, Ld, d, dtype", [
+    (4, 32, 9, 77, 128, torch.float16),     # odd B: each query's last pair holds one doc
+    (5, 32, 10, 77, 128, torch.bfloat16),
+    (3, 128, 7, 300, 128, torch.float16),   # full query tile: pairs at any doc length
+    (6, 24, 5, 60, 96, torch.float16),      # masked width
+])
+def test_per_query_docs_pairs(oracle_mod, Nq, Lq, B, Ld, d, dtype):
+    # Per-query docs score two of one query's docs per workgroup.
+    Q = sim((Nq, Lq, d), 230 + Lq, dtype)
+    D = sim((Nq, B, Ld, d), 231 + B, dtype)
+    lengths = torch.randint(0, Ld + 3, (Nq * B,), generator=torch.Generator().manual_seed(Nq * B), dtype=torch.int32)
+    lengths[1] = 0
+    out = fm.flash_maxsim_batched(Q.to(DEV), D.to(DEV), lengths.to(DEV), shared_docs=False)
+    ref = oracle_mod.maxsim(to_np32(Q), to_np32(D.reshape(Nq * B, Ld, d)), lengths.numpy(), shared_docs=False)
+    assert out.shape == (Nq, B)
+    assert_scores(out, ref)
+
+
 def test_batched_large_query(oracle_mod):
     Q = sim((3, 300, 128), 220)
     D = sim((6, 80, 128), 221)
