@@ -46,9 +46,10 @@ constexpr int stream_depth() {
 
 // KMASK: d is not exactly 32*KS, so fragment slots past d must read as zero.
 // VEC: uint8 vector load path (FwdArgs::vec); true for fp16/bf16.
-// DOCS = 2 (single query, one pass, no argmax; uint8 docs, and fp16/bf16 docs
-// with a full 128-VGPR query tile or of up to 256 tokens): the workgroup scores docs
-// 2x and 2x+1 as one tile sequence (the first doc's tiles, then the second's),
+// DOCS = 2 (one pass, no argmax; uint8 docs of one query, and fp16/bf16 docs
+// of one query or per-query docs, with a full 128-VGPR query tile or of up to
+// 256 tokens): the workgroup scores docs 2p and 2p+1 of a query as one tile
+// sequence (the first doc's tiles, then the second's),
 // so its query tile, row sums and load ring carry over from one doc to the
 // next instead of being rebuilt and refilled per doc.
 // JOINT (two uint8 docs with aligned rows): one buffer range covers the
@@ -500,6 +501,8 @@ hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
     // shared by two docs (Lq = 32: 64-token docs 46.8 -> 32.4 us, 77 tokens
     // 26.7 -> 19.9 us, 160 tokens 60.9 -> 52.6 us; Lq = 16 and 64 over
     // 77-token docs -26 % and -17 %; d = 96: 77 tokens -30 %, 128 -22 %).
+    // Per-query docs pair two of one query's docs (100 queries x 1000 docs
+    // of 77 tokens: 577 -> 376 us).
     constexpr bool BIG = NQB * KS >= 32;
     if ((a.Nq == 1 || !a.shared_docs) && npass == 1 && !a.qidx && (BIG ? !KMASK : a.Ld <= 256)) {
       hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2>),
