@@ -99,10 +99,14 @@ stream_fwd_kernel(FwdArgs a) {
   int qi, b;
   if constexpr (DOCS == 2) {
     // workgroup xi: docs 2p and 2p + 1 of query qi (per-query docs: that
-    // query's own docs, rows qi * B + b)
-    const int pairs = (a.B + 1) / 2;
-    qi = xi / pairs;
-    b = 2 * (xi - qi * pairs);
+    // query's own docs, rows qi * B + b); a single query skips the division
+    qi = 0;
+    b = 2 * xi;
+    if (!U8 && a.Nq > 1) {
+      const int pairs = (a.B + 1) / 2;
+      qi = xi / pairs;
+      b = 2 * (xi - qi * pairs);
+    }
   } else if (a.shared_docs && a.Nq > 1) {
     // Queries of one doc run back to back so the doc streams from HBM once
     // and the other queries find it in cache.
