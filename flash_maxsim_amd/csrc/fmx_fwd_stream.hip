@@ -112,6 +112,9 @@ stream_fwd_kernel(FwdArgs a) {
     // and the other queries find it in cache.
     b = xi / a.Nq;
     qi = xi - b * a.Nq;
+  } else if (a.Nq == 1) {
+    qi = 0;  // no integer division (a few dozen instructions) before the first loads
+    b = xi;
   } else {
     qi = xi / a.B;
     b = xi - qi * a.B;
