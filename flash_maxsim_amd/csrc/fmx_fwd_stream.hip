@@ -68,10 +68,11 @@ constexpr int stream_min_waves() {
   return (KIND == KIND_U8 && NQB * KS >= 32) ? 2 : 1;
 }
 
-template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX, bool VEC, int DOCS = 1, bool JOINT = false>
+// PD: ring depth other than stream_depth's (0: stream_depth's).
+template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX, bool VEC, int DOCS = 1, bool JOINT = false, int PD = 0>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(stream_min_waves<KIND, NQB, KS, VEC, DOCS>())))
 stream_fwd_kernel(FwdArgs a) {
-  constexpr int NW = kStreamWaves, P = stream_depth<KIND, NQB, KS>(), QROWS = NQB * 16;
+  constexpr int NW = kStreamWaves, P = PD ? PD : stream_depth<KIND, NQB, KS>(), QROWS = NQB * 16;
   constexpr int ESZ = KindInfo<KIND>::esz;
   constexpr bool BF = KindInfo<KIND>::bf;
   constexpr bool U8 = KIND == KIND_U8;
@@ -489,7 +490,16 @@ hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
       // pair of padded scale rows, or the whole packed scale array.
       const int64_t sm_rows = a.tok_group ? a.tok_rows : a.sm_b + a.Ld;
       constexpr bool GROUPS = VEC && stream_depth<KIND, NQB, KS>() == 4;  // group scale loads
-      if (GROUPS && sm_rows * 2 + 64 < ((int64_t)1 << 31)) {
+      if (a.Ld <= 128) {
+        // Docs of up to 128 tokens: a two-tile ring (per-tile scale loads).
+        // The deeper ring's fixed refill pattern issues loads past a short
+        // pair's tiles and its fill is paid per workgroup (5000 docs of 77
+        // tokens: 22.0 -> 19.3 us, 20000: 77.9 -> 65.5 us, a 64-token query
+        // -20 %, 128-token docs -5 %); longer docs keep it (200 tokens: +4 %
+        // with two tiles, config 4: +7.5 %).
+        hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2, false, 2>), grid, dim3(256), 0, s,
+                           a);
+      } else if (GROUPS && sm_rows * 2 + 64 < ((int64_t)1 << 31)) {
         hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2, GROUPS>), grid, dim3(256), 0, s, a);
       } else {
         hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2>), grid, dim3(256), 0, s, a);

@@ -66,3 +66,20 @@ def test_per_query_doc_routes(oracle_mod, Lq, Ld, d, B, i):
     out = fm.flash_maxsim_batched(Q.to(DEV), D.to(DEV), lengths.to(DEV), shared_docs=False)
     ref = oracle_mod.maxsim(to_np32(Q), to_np32(D.reshape(Nq * B, Ld, d)), lengths.numpy(), shared_docs=False)
     _check(out, ref)
+
+
+@pytest.mark.parametrize("Lq, Ld, d, B", [(32, 77, 128, 9), (64, 128, 128, 6), (32, 129, 128, 7),
+                                          (32, 200, 128, 5), (16, 64, 96, 8), (48, 100, 128, 11)])
+def test_int8_doc_length_routes(oracle_mod, Lq, Ld, d, B):
+    # uint8 docs of up to 128 tokens run a two-tile ring, longer ones the
+    # four-tile ring with group scale loads (aligned rows) or per-tile loads.
+    seed = 1200 + Lq + Ld
+    Q = sim((Lq, d), seed)
+    x = sim((B, Ld, d), seed + 1, torch.float32)
+    codes, s, m = fm.quantize_int8(x)
+    lengths = torch.randint(0, Ld + 2, (B,), generator=torch.Generator().manual_seed(seed), dtype=torch.int32)
+    lengths[0] = Ld
+    if B > 3:
+        lengths[2] = 0
+    out = fm.flash_maxsim_int8(Q.to(DEV), codes.to(DEV), s.to(DEV), m.to(DEV), lengths.to(DEV))
+    _check(out, oracle_mod.maxsim_int8(to_np32(Q), codes.numpy(), to_np32(s), to_np32(m), lengths.numpy()))
