@@ -26,7 +26,9 @@ Configs (the driver's line is the default, c1):
 --rotate R (R >= 2) cycles R copies of the doc tensor(s) for any config.
 --doc-align A (c4_packed) starts each packed doc on a multiple of A token rows.
 Any single-query shape: s_Lq_B_Ld_d (fp16 docs) or u8_Lq_B_Ld_d (quantize_int8
-codes of the same random docs), e.g. s_32_5000_1024_128.
+codes of the same random docs), e.g. s_32_5000_1024_128; several fp16 queries:
+b_Nq_Lq_B_Ld_d (docs shared by all queries) or p_Nq_Lq_B_Ld_d (each query its own
+B docs), e.g. p_100_32_1000_77_128.
 
 roofline: the dominant kernel's algorithmic bytes (or flops) per launch divided
 by its average launch duration, timed with HIP events recorded on the stream
@@ -354,6 +356,41 @@ def build(name: str, rotate: int, doc_align: int = 4) -> Workload:
         roof = ({"bound": "mfma", "amount": flops, "unit": "TFLOP/s", "kernel": "forward"} if mfma else
                 {"bound": "hbm", "amount": amount, "unit": "GB/s", "kernel": "forward"})
         return Workload(cfg, steps, B, "docs/s", roof, cpu, n, f"maxsim_naive fp32 over the first {n} docs")
+
+    shape = re.fullmatch(r"(p|b)_(\d+)_(\d+)_(\d+)_(\d+)_(\d+)", name)
+    if shape:  # several queries: p_ (per-query docs) or b_ (docs shared by all queries)
+        kind = shape.group(1)
+        Nq, Lq, B, Ld, d = map(int, shape.groups()[1:])
+        Q = sim((Nq, Lq, d), 63, f16)
+        Qd, Qc = Q.to(dev), Q.float()
+        n = min(B, 50)
+        nq = min(Nq, 4)
+        if kind == "p":
+            Dh = sim((Nq, B, Ld, d), 64, f16)
+            Ds = _copies(Dh.to(dev), rotate)
+            steps = [lambda D=D: fm.flash_maxsim_batched(Qd, D, None, False) for D in Ds]
+            Dc = Dh[:nq, :n].float()
+            cpu = lambda: [fm.maxsim_naive(Qc[i], Dc[i]) for i in range(nq)]  # noqa: E731
+            amount = Nq * B * Ld * d * 2 + Nq * Lq * d * 2 + Nq * B * 4
+            what, docs = "per-query docs", f"D[{Nq},{B},{Ld},{d}]"
+        else:
+            Dh = sim((B, Ld, d), 64, f16)
+            Ds = _copies(Dh.to(dev), rotate)
+            steps = [lambda D=D: fm.flash_maxsim_batched(Qd, D) for D in Ds]
+            Dc = Dh[:n].float()
+            cpu = lambda: [fm.maxsim_naive(Qc[i], Dc) for i in range(nq)]  # noqa: E731
+            amount = B * Ld * d * 2 + Nq * Lq * d * 2 + Nq * B * 4
+            what, docs = "shared docs", f"D[{B},{Ld},{d}]"
+        flops = 2 * Nq * Lq * B * Ld * d
+        cfg = {"workload": f"batched flash_maxsim Q[{Nq},{Lq},{d}] x {docs} fp16 {what}", "Nq": Nq, "B": B,
+               "Lq": Lq, "Ld": Ld, "d": d}
+        if rotate > 1:
+            cfg["rotated_doc_copies"] = len(steps)
+        mfma = flops / MFMA_F16_PEAK_TFLOPS / 1e12 > amount / HBM_PEAK_GBS / 1e9
+        roof = ({"bound": "mfma", "amount": flops, "unit": "TFLOP/s", "kernel": "forward"} if mfma else
+                {"bound": "hbm", "amount": amount, "unit": "GB/s", "kernel": "forward"})
+        return Workload(cfg, steps, Nq * B, "pairs/s", roof, cpu, nq * n,
+                        f"maxsim_naive fp32, {nq} queries x the first {n} docs")
 
     raise SystemExit(f"unknown config {name}")
 
