@@ -12,8 +12,11 @@ Differences by design:
     fp16 (any other dtype mix is cast to fp16 as in the reference);
   * doc_lengths are clamped to [0, Ld] on the GPU (the reference reads past the
     doc for lengths > Ld) and must have one entry per doc row;
-  * a d that is not a multiple of 8 is zero-padded to one (a copy) because the
-    kernels read rows with 16-byte loads.
+  * operands are read in place when their row strides are multiple of 8
+    elements (d masked in the kernels), so D = store[..., :d] of a store padded
+    to a multiple of 8 costs no copy; other layouts, and contiguous rows with
+    d % 8 != 0, are copied once per call with d zero-padded to a multiple of 8
+    (the kernels read rows with 16-byte loads).
 """
 
 from __future__ import annotations
@@ -47,8 +50,23 @@ def _kernel_dtype(*tensors: torch.Tensor) -> torch.dtype:
     return torch.bfloat16 if all(t.dtype == torch.bfloat16 for t in tensors) else torch.float16
 
 
+def _abi_ready(t: torch.Tensor, dtype: torch.dtype | None) -> bool:
+    """True when the kernels can read t in place: kernel dtype, unit stride
+    along d, every other stride a multiple of 8 elements and at least d along
+    rows, 16-byte aligned. The kernels mask elements at or past d, so rows of a
+    wider buffer (t = buf[..., :d]) need no copy even when d % 8 != 0."""
+    if t.dim() < 2 or (dtype is not None and t.dtype != dtype):
+        return False
+    if t.stride(-1) != 1 or t.stride(-2) < t.shape[-1] or t.data_ptr() % 16:
+        return False
+    return all(s % 8 == 0 for s in t.stride()[:-1])
+
+
 def _prep(t: torch.Tensor, dtype: torch.dtype | None) -> torch.Tensor:
-    """Contiguous, cast, d padded to a multiple of 8, 16-byte aligned."""
+    """t itself when the kernels can read it in place, else a contiguous cast
+    copy with d zero-padded to a multiple of 8, 16-byte aligned."""
+    if _abi_ready(t, dtype):
+        return t
     t = t.contiguous()
     if dtype is not None and t.dtype != dtype:
         t = t.to(dtype)
@@ -72,8 +90,9 @@ def _lengths(total: int, device: torch.device, doc_lengths) -> torch.Tensor | No
 def _launch_fwd(Q, D, lengths, Nq, B, Lq, Ld, d, shared_docs, save_argmax):
     """Scores [Nq, B] fp32 (+ argmax [Nq*B, Lq] int32) from prepared operands.
 
-    Q is [Nq, Lq, dp] or [Lq, dp], D is [B', Ld, dp] with dp = d rounded up to
-    8; mirrors _launch_fwd (reference flash_maxsim.py:195-208).
+    Q is [Nq, Lq, d'] or [Lq, d'], D is [B', Ld, d'] with d' >= d (the
+    kernels read the first d elements of each row; strides as _prep leaves
+    them); mirrors _launch_fwd (reference flash_maxsim.py:195-208).
     """
     dev = _check_devices(Q, D, lengths)
     lib = _lib.load()

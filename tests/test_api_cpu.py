@@ -233,6 +233,37 @@ def test_python_api_refuses_cpu_tensors():
         fm.flash_maxsim_train(Q, D)
 
 
+def test_operand_prep_reads_abi_layouts_in_place():
+    """Views the C ABI accepts (row strides multiple of 8 and >= d, unit stride
+    along d, 16-byte aligned, kernel dtype) pass through uncopied, d % 8 != 0
+    included; everything else becomes a zero-padded contiguous copy."""
+    from flash_maxsim_amd.flash_maxsim import _prep
+
+    f16 = torch.float16
+    store = torch.full((6, 40, 104), float("nan"), dtype=f16)
+    view = store[1:5, :33, :100]                     # padded store, d = 100
+    assert _prep(view, f16) is view
+    q = torch.zeros(64, 136, dtype=f16)[::2, :128]   # strided rows
+    assert _prep(q, f16) is q
+    codes = torch.zeros(4, 40, 112, dtype=torch.uint8)[:, :, :100]  # uint8 codes, no cast
+    assert _prep(codes, None) is codes
+
+    for t, dt in [(torch.zeros(3, 10, 100, dtype=f16), f16),            # contiguous, d % 8 != 0
+                  (torch.zeros(3, 128, 64, dtype=f16).transpose(1, 2), f16),
+                  (store[:, :, 4:100], f16),                            # 8-byte aligned base
+                  (store[:, :, :100], torch.bfloat16)]:                 # needs a cast
+        out = _prep(t, dt)
+        assert out.data_ptr() != t.data_ptr() or out.dtype != t.dtype
+        assert out.is_contiguous() and out.shape[-1] % 8 == 0 and out.data_ptr() % 16 == 0
+        assert out.dtype == dt
+        d = t.shape[-1]
+        torch.testing.assert_close(out[..., :d].float(), t.float().to(dt).float(), equal_nan=True)
+        assert not out[..., d:].float().any()
+    # overlapping rows (row stride 8 < d = 96) are copied, not passed through
+    ov = torch.zeros(3 * 10 * 96, dtype=f16).as_strided((3, 10, 96), (960, 8, 1))
+    assert _prep(ov, f16).stride(-2) == 96
+
+
 def test_naive_functions_run_on_cpu():
     import flash_maxsim_amd as fm
 
