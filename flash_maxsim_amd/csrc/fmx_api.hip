@@ -158,7 +158,7 @@ size_t fmx_fwd_workspace_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t Ld, in
 
 size_t fmx_fwd_int8_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld, int64_t d) {
   (void)Ld;
-  return stream_ws_bytes(1, B, Lq, d);
+  return fwd_ws_bytes(1, B, Lq, d);  // the streaming, split-d and tiled kernels all take uint8 docs
 }
 
 }  // extern "C"
@@ -253,7 +253,15 @@ int int8_impl(const void* Q, int64_t q_stride_l, const uint8_t* D, int64_t d_str
     return fail(FMX_ERR_INVALID, "scales and mins must be 2-byte aligned");
   if (!tok_group && sm_stride_b < Ld)
     return fail(FMX_ERR_INVALID, "scale doc stride %lld < Ld", (long long)sm_stride_b);
-  const size_t need = stream_ws_bytes(1, B, Lq, d);
+  const bool tiled = d <= 256 && fmx::tiled_u8_applicable(Lq, Ld, (int)d);
+  fmx::TiledPlan tp = {};
+  size_t need;
+  if (tiled) {
+    tp = fmx::tiled_fwd_plan(1, B, Lq, (int)d, device_cus());
+    need = fmx::tiled_fwd_workspace_bytes(tp, 1, B);
+  } else {
+    need = stream_ws_bytes(1, B, Lq, d);
+  }
   if (need > 0 && (!workspace || workspace_bytes < need))
     return fail(FMX_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
 
@@ -290,8 +298,9 @@ int int8_impl(const void* Q, int64_t q_stride_l, const uint8_t* D, int64_t d_str
   const bool rows16 = (d_stride_l & 15) == 0 && (tok_group || (d_stride_b & 15) == 0);
   a.vec = (rows16 && sm8 && (tok_group || ((sm_stride_b & 3) == 0 && (Ld & 3) == 0))) ? 1 : 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const hipError_t e = plan_fwd(Lq, d).splitd ? fmx::launch_splitd_fwd(fmx::KIND_U8, a, false, s)
-                                              : fmx::launch_stream_fwd(fmx::KIND_U8, a, false, s);
+  const hipError_t e = tiled                   ? fmx::launch_tiled_fwd(fmx::KIND_U8, a, tp, false, s)
+                       : plan_fwd(Lq, d).splitd ? fmx::launch_splitd_fwd(fmx::KIND_U8, a, false, s)
+                                                : fmx::launch_stream_fwd(fmx::KIND_U8, a, false, s);
   return hip_status(e, "fmx_fwd_int8 launch");
 }
 
@@ -387,7 +396,7 @@ int fmx_fwd_packed(int dtype, const void* Q, int64_t q_stride_l, int64_t Lq, con
 }
 
 size_t fmx_fwd_int8_packed_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld_max, int64_t d) {
-  return stream_ws_bytes(1, B, Lq, d);
+  return fwd_ws_bytes(1, B, Lq, d);
 }
 
 int fmx_fwd_int8_packed(const void* Q, int64_t q_stride_l, int64_t Lq, const uint8_t* codes, int64_t c_stride_l,

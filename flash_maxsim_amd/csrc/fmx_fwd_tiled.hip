@@ -20,6 +20,13 @@
 // a query inside the row block is written to scores, a query straddling row
 // blocks to a partial slot that a second kernel adds in row-block order.
 //
+// uint8 docs (single queries, reference flash_maxsim_quant.py:60-101) take
+// the same path: each chunk of eight codes is dequantised to fp16 (code *
+// scale + min, one fp16 rounding, as the reference's kernel dequantises before
+// its dot product, flash_maxsim_quant.py:89) while it moves from the staging
+// registers to LDS, so the tile in LDS and every step after it are the fp16
+// kernel's, and the scores equal the fp16 path's on the dequantised docs.
+//
 // blockIdx -> (row block, doc group) is XCD-aware when the plan says so: the
 // eight XCDs take workgroups round-robin, so all row blocks of doc group g are
 // put on XCD g % 8 and read each doc tile through the same L2.
@@ -108,6 +115,41 @@ __device__ __forceinline__ void fold_rows(f32x4_t acc, int rowj, int len, bool t
   }
 }
 
+// uint8 docs: a chunk of eight codes in registers with the fp16 bits of its
+// token's scale (low half) and min (high half).
+struct U8Chunk {
+  u32x2_t codes;
+  uint32_t sm;
+};
+
+// Buffer resources of the doc a tile comes from: token rows, and for uint8
+// docs the doc's scales and mins (else copies of d, unused).
+struct TileRes {
+  rsrc_t d, s, m;
+};
+
+// Eight uint8 codes dequantised to fp16 as the reference's int8 kernel does
+// before its dot product (flash_maxsim_quant.py:89, code * scale + min in
+// fp16): code c is exact as fp16 (1024 + c, less 1024), then one fp16 fma
+// rounds c * scale + min once.
+__device__ __forceinline__ u32x4_t dequant8_f16(u32x2_t codes, uint32_t sm) {
+  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+  const h2_t sc = __builtin_bit_cast(h2_t, (sm & 0xffffu) * 0x10001u);
+  const h2_t mn = __builtin_bit_cast(h2_t, (sm >> 16) * 0x10001u);
+  const h2_t bias = {(_Float16)kCodeBias, (_Float16)kCodeBias};
+  const u32x4_t h = codes_to_f16_biased(codes);
+  u32x4_t o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // bit_cast a copy: clang casts the first element for a vector subscript
+    const uint32_t hi = h[i];
+    const h2_t c = __builtin_bit_cast(h2_t, hi) - bias;
+    const uint32_t v = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, sc, mn));
+    o[i] = v;
+  }
+  return o;
+}
+
 // Workgroup barrier once this wave's LDS accesses have completed, without
 // the workgroup fence of __syncthreads(), which also waits for every vector
 // memory load in flight (vmcnt(0)). The empty asm statements keep the
@@ -136,9 +178,16 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
   // waits for the one tile in flight (Nq = 2 x 32 tokens over 5000 docs:
   // 92.5 -> 82.2 us). From 32 rows per wave on, the VGPR staging and LDS
   // stores cost more than the deeper ring gains (Nq = 8 x 32: +3 %).
+  // uint8 docs (single queries, no argmax) always stage through VGPRs, where
+  // each chunk of eight codes is dequantised to fp16 on its way to LDS; the
+  // MFMA and everything after it are the fp16 kernel's.
+  constexpr bool U8 = KIND == KIND_U8;
+  static_assert(!(U8 && ARGMAX), "uint8 docs are scored without argmax");
+  constexpr int ESZ = KindInfo<KIND>::esz;
+  using stage_t = std::conditional_t<U8, U8Chunk, u32x4_t>;
   constexpr bool RING = !ARGMAX && NB == 1 && KS == 4;
   constexpr int PR = 4;
-  constexpr bool DMA = !KMASK && !ARGMAX && !RING;
+  constexpr bool DMA = !KMASK && !ARGMAX && !RING && !U8;
   constexpr int ROWB = 64 * KS + (DMA ? 0 : 16);  // LDS bytes per token row
   constexpr int BUFB = TJ * ROWB;          // LDS bytes per tile buffer
   constexpr int CPR = 4 * KS;              // 16-byte chunks per token row
@@ -206,51 +255,76 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
   }
 
   // ---- tile loader: chunk k of this thread = tid + k*512 -> (row, 16-byte column) ----
-  const uint32_t rowb = (uint32_t)(a.sd_l * 2);
+  const uint32_t rowb = (uint32_t)(a.sd_l * ESZ);
   auto tile_rsrc = [&](int b, int len) {
     int64_t rows = len;
     const char* base = static_cast<const char*>(a.D);
+    int64_t sm0 = 0;  // uint8: first scale / min of the doc
     if (a.tok_group) {  // packed docs: clamp to the rows of D
       const int64_t t0 = 4 * ld_uniform(a.tok_group + b);
       const int64_t avail = t0 < 0 ? 0 : (a.tok_rows > t0 ? a.tok_rows - t0 : 0);
       if (rows > avail) rows = avail;
-      if (avail > 0) base += t0 * a.sd_l * 2;
+      if (avail > 0) {
+        base += t0 * a.sd_l * ESZ;
+        sm0 = t0;
+      }
     } else {
-      base += doc_elem0(a, b) * 2;
+      base += doc_elem0(a, b) * ESZ;
+      sm0 = (int64_t)b * a.sm_b;
     }
-    return make_rsrc(base, (uint32_t)rows * rowb);
+    TileRes r;
+    r.d = make_rsrc(base, (uint32_t)rows * rowb);
+    if constexpr (U8) {
+      r.s = make_rsrc(a.scales + sm0, (uint32_t)rows * 2u);
+      r.m = make_rsrc(a.mins + sm0, (uint32_t)rows * 2u);
+    } else {
+      r.s = r.d;
+      r.m = r.d;
+    }
+    return r;
   };
   auto doc_len = [&](int b) {
     int l = a.lengths ? ld_uniform(a.lengths + b) : a.Ld;
     return l < 0 ? 0 : (l > a.Ld ? a.Ld : l);
   };
-  u32x4_t stage[CPT];
-  auto load_tile_regs = [&](u32x4_t (&dst)[CPT], rsrc_t rd, int t) __attribute__((always_inline)) {
+  stage_t stage[CPT];
+  auto load_tile_regs = [&](stage_t (&dst)[CPT], const TileRes& rd, int t) __attribute__((always_inline)) {
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int chunk = tid + k * NW * 64;
       const int row = chunk / CPR, cc = chunk - (chunk / CPR) * CPR;
       const int e0 = cc * 8;
-      uint32_t off = (uint32_t)(t * TJ + row) * rowb + (uint32_t)(e0 * 2);
+      uint32_t off = (uint32_t)(t * TJ + row) * rowb + (uint32_t)(e0 * ESZ);
       if (KMASK && e0 >= a.d) off = kOOB;
-      dst[k] = ld16(rd, off);
+      if constexpr (U8) {
+        const uint32_t so = (uint32_t)(t * TJ + row) * 2u;
+        dst[k].codes = ld8(rd.d, off);
+        dst[k].sm = (uint32_t)ld2(rd.s, so) | ((uint32_t)ld2(rd.m, so) << 16);
+      } else {
+        dst[k] = ld16(rd.d, off);
+      }
     }
   };
   // The partial 8-wide chunk (d % 8 != 0) is masked here, when the loaded
   // value is used anyway, so a load is never waited for right after issue.
-  auto store_tile_lds = [&](const u32x4_t (&src)[CPT], unsigned char* dst) __attribute__((always_inline)) {
+  auto store_tile_lds = [&](const stage_t (&src)[CPT], unsigned char* dst) __attribute__((always_inline)) {
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int chunk = tid + k * NW * 64;
       const int row = chunk / CPR, cc = chunk - (chunk / CPR) * CPR;
-      u32x4_t v = src[k];
+      u32x4_t v;
+      if constexpr (U8) {
+        v = dequant8_f16(src[k].codes, src[k].sm);
+      } else {
+        v = src[k];
+      }
       if (has_partial && cc * 8 == kp) v &= prefix_mask16(a.d & 7);
       *reinterpret_cast<u32x4_t*>(dst + row * ROWB + cc * 16) = v;
     }
   };
   // DMA: instruction k of wave w fills chunk positions (k*NW + w)*64 .. +63 of
   // the buffer; lane l's position holds column (position % CPR) ^ (row % 16).
-  auto dma_tile = [&](rsrc_t rd, int t, unsigned char* dst) {
+  auto dma_tile = [&](const TileRes& rd, int t, unsigned char* dst) {
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int slot = (k * NW + wave) * 64 + lane;
@@ -258,7 +332,7 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
       const int col = pos ^ (row & 15);
       const uint32_t off = (uint32_t)(t * TJ + row) * rowb + (uint32_t)(col * 16);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rd, (__attribute__((address_space(3))) void*)(dst + (k * NW + wave) * 1024), 16, off, 0, 0, 0);
+          rd.d, (__attribute__((address_space(3))) void*)(dst + (k * NW + wave) * 1024), 16, off, 0, 0, 0);
     }
   };
   // Every wave's DMA writes of the next tile are in LDS before the barrier.
@@ -278,7 +352,7 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
   int b = grp;
   int len = doc_len(b);
   int nt = len > 0 ? (len + TJ - 1) / TJ : 1;  // an empty doc still takes one fully masked tile
-  rsrc_t rd = tile_rsrc(b, len);
+  TileRes rd = tile_rsrc(b, len);
   int t = 0, par = 0;
 
   // Tile t of doc b from the LDS tile at base, folded into the running maxima.
@@ -426,11 +500,12 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
     // no memory access), so every step issues the same loads and the compiler
     // waits for exactly the slot it stores. The barrier skips the workgroup
     // fence of __syncthreads(), whose vmcnt(0) would drain the ring.
-    u32x4_t ring[PR][CPT];
+    stage_t ring[PR][CPT];
     int pb = b, pt = 0, pnt = nt;
-    rsrc_t prd = rd;
-    const rsrc_t nul = make_rsrc(a.D, 0u);
-    auto fetch = [&](u32x4_t (&dst)[CPT]) __attribute__((always_inline)) {
+    TileRes prd = rd;
+    const rsrc_t z = make_rsrc(a.D, 0u);
+    const TileRes nul = {z, z, z};
+    auto fetch = [&](stage_t (&dst)[CPT]) __attribute__((always_inline)) {
       const bool have = pb < a.B;
       load_tile_regs(dst, have ? prd : nul, pt);
       if (!have) return;
@@ -489,7 +564,7 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
         nt_tile = 0;
       }
       const bool has_next = nb_doc < a.B;
-      rsrc_t rd_next = rd;
+      TileRes rd_next = rd;
       if (has_next) {
         if (nb_doc != b) {
           nlen = doc_len(nb_doc);
@@ -528,7 +603,7 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
         nt_tile = 0;
       }
       const bool has_next = nb_doc < a.B;
-      rsrc_t rd_next = rd;
+      TileRes rd_next = rd;
       if (has_next) {
         if (nb_doc != b) {
           nlen = doc_len(nb_doc);
@@ -584,10 +659,15 @@ hipError_t launch_one(const FwdArgs& a, const TiledPlan& p, hipStream_t s) {
 template <int KIND, int NW, int NB, int KS>
 hipError_t dispatch_flags(const FwdArgs& a, const TiledPlan& p, bool am, hipStream_t s) {
   const bool kmask = a.d != 32 * KS;
-  if (kmask) {
-    return am ? launch_one<KIND, NW, NB, KS, true, true>(a, p, s) : launch_one<KIND, NW, NB, KS, true, false>(a, p, s);
+  if constexpr (KIND == KIND_U8) {
+    if (am) return hipErrorInvalidValue;
+    return kmask ? launch_one<KIND, NW, NB, KS, true, false>(a, p, s) : launch_one<KIND, NW, NB, KS, false, false>(a, p, s);
+  } else {
+    if (kmask) {
+      return am ? launch_one<KIND, NW, NB, KS, true, true>(a, p, s) : launch_one<KIND, NW, NB, KS, true, false>(a, p, s);
+    }
+    return am ? launch_one<KIND, NW, NB, KS, false, true>(a, p, s) : launch_one<KIND, NW, NB, KS, false, false>(a, p, s);
   }
-  return am ? launch_one<KIND, NW, NB, KS, false, true>(a, p, s) : launch_one<KIND, NW, NB, KS, false, false>(a, p, s);
 }
 
 template <int KIND>
@@ -641,6 +721,21 @@ bool tiled_fwd_applicable(int64_t Nq, int64_t Lq, int64_t Ld, int d) {
   if (d < 1 || d > 256) return false;
   if (Nq > 1 || Lq > 16 * stream_fwd_nqb(1 << 20, d)) return true;
   return d <= 128 && ((Lq > 32 && Ld <= 96) || (Lq > 64 && Ld <= 160));
+}
+
+// uint8 docs (single queries): the tiled kernel from 65 query rows over docs
+// of up to 128 tokens, and at d <= 128 from 129 rows (several streaming
+// passes) over docs of up to 512 tokens. 5000 docs of 77 tokens: 128 rows
+// 45.7 -> 31.4 us, 80 rows 43.2 -> 30.6, 256 rows 102.0 -> 42.9, d = 256
+// 130.4 -> 90.1; 128 rows over 64/96/128 tokens -21/-7/-6 %; 200/300/512
+// rows over 300 tokens -17/-6/-20 %. The streaming kernel stays faster for 64
+// rows over 77 tokens (24.7 against 29.3 us), 128 rows over 200 tokens (-5 %),
+// 512 rows over 1024 tokens (-8 %), 128 rows over 300 tokens at d = 256 (67.0
+// against 104.6 us) and any query of up to 64 rows over longer docs.
+bool tiled_u8_applicable(int64_t Lq, int64_t Ld, int d) {
+  if (d < 1 || d > 256 || Lq <= 64) return false;
+  if (Ld <= 128) return true;
+  return d <= 128 && Lq > 16 * stream_fwd_nqb(1 << 20, d) && Ld <= 512;
 }
 
 bool tiled_fwd_possible(int64_t Nq, int64_t Lq, int d) {
@@ -730,6 +825,7 @@ hipError_t launch_tiled_fwd(int kind, const FwdArgs& a, const TiledPlan& p, bool
   switch (kind) {
     case KIND_F16: return dispatch<KIND_F16>(a, p, with_argmax, s);
     case KIND_BF16: return dispatch<KIND_BF16>(a, p, with_argmax, s);
+    case KIND_U8: return dispatch<KIND_U8>(a, p, with_argmax, s);
     default: return hipErrorInvalidValue;
   }
 }

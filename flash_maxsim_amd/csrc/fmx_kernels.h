@@ -72,8 +72,9 @@ int splitd_fwd_passes(int Lq, int d); // > 1: partial sums in FwdArgs::partial
 hipError_t launch_splitd_fwd(int kind, const FwdArgs& a, bool with_argmax, hipStream_t s);
 
 // Tiled kernel (MFMA-bound regime): persistent 8- or 4-wave workgroups keep a
-// block of query rows in VGPRs and stream shared docs through LDS. d <= 256
-// and at least 256 query rows in total.
+// block of query rows in VGPRs and stream shared docs through LDS. d <= 256.
+// fp16/bf16 docs, and uint8 docs (dequantised to fp16 on their way to LDS;
+// single queries, no argmax).
 struct TiledPlan {
   int ks;              // 32-wide k-steps (4: d <= 128, 8: d <= 256)
   int nw;              // waves per workgroup (8, or 4 with three workgroups per CU)
@@ -87,6 +88,7 @@ struct TiledPlan {
 };
 bool tiled_fwd_applicable(int64_t Nq, int64_t Lq, int64_t Ld, int d);  // fmx_fwd's choice
 bool tiled_fwd_possible(int64_t Nq, int64_t Lq, int d);                 // for some Ld (workspace bounds)
+bool tiled_u8_applicable(int64_t Lq, int64_t Ld, int d);                 // fmx_fwd_int8's choice (single query)
 TiledPlan tiled_fwd_plan(int64_t Nq, int64_t B, int64_t Lq, int d, int cus);
 size_t tiled_fwd_workspace_bytes(const TiledPlan& p, int64_t Nq, int64_t B);
 hipError_t launch_tiled_fwd(int kind, const FwdArgs& a, const TiledPlan& p, bool with_argmax, hipStream_t s);

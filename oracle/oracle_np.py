@@ -8,6 +8,9 @@ tests/test_oracle.py, so that a slip in either shows up.
                  batched :233-250, sparse flash_maxsim_sparse.py:153-157)
   quantize_np    flash_maxsim/flash_maxsim_quant.py:23-28 (float32 arithmetic)
   dequantize_np  flash_maxsim/flash_maxsim_quant.py:31-33
+  dequantize_fp16_np
+                 flash_maxsim/flash_maxsim_quant.py:89 (the kernel's fp16
+                 dequantisation before its dot product)
   bwd_np         flash_maxsim/flash_maxsim.py:153-188
 """
 
@@ -70,6 +73,18 @@ def dequantize_np(codes, scales, mins):
     """codes * scale + min in float32, as torch's dequantize_int8."""
     return (np.asarray(codes).astype(np.float32) * np.asarray(scales, dtype=np.float32)
             + np.asarray(mins, dtype=np.float32))
+
+
+def dequantize_fp16_np(codes, scales, mins):
+    """codes * scale + min rounded once to fp16 (float16 array).
+
+    The product and sum are exact in float64 (an 8-bit code times an 11-bit
+    significand, plus an fp16 min, spans fewer than 53 bits), so the cast is
+    the single round-to-nearest-even of the exact value."""
+    exact = (np.asarray(codes).astype(np.float64) * np.asarray(scales, dtype=np.float16).astype(np.float64)
+             + np.asarray(mins, dtype=np.float16).astype(np.float64))
+    with np.errstate(over="ignore"):  # past the fp16 range: inf, as the hardware rounds
+        return exact.astype(np.float16)
 
 
 def bwd_np(Q, D, argmax, grad):

@@ -83,3 +83,39 @@ def test_int8_doc_length_routes(oracle_mod, Lq, Ld, d, B):
         lengths[2] = 0
     out = fm.flash_maxsim_int8(Q.to(DEV), codes.to(DEV), s.to(DEV), m.to(DEV), lengths.to(DEV))
     _check(out, oracle_mod.maxsim_int8(to_np32(Q), codes.numpy(), to_np32(s), to_np32(m), lengths.numpy()))
+
+
+@pytest.mark.parametrize("Lq, Ld, d, B, tiled", [
+    (64, 77, 128, 9, False),     # 64 rows: streamed
+    (65, 77, 128, 9, True),      # 65 rows over short docs: tiled
+    (128, 128, 128, 7, True),
+    (128, 129, 128, 7, False),   # 65-128 rows over longer docs: streamed
+    (129, 300, 128, 6, True),    # several streaming passes over mid-length docs: tiled
+    (129, 513, 128, 5, False),
+    (100, 96, 120, 8, True),     # masked width
+    (300, 64, 100, 5, True),     # partial 8-wide chunk, queries straddling row blocks
+    (128, 77, 256, 6, True),     # d = 256 over short docs
+    (129, 300, 256, 5, False),   # d = 256 over longer docs: streamed (split into passes)
+])
+def test_int8_tiled_routes(oracle_mod, Lq, Ld, d, B, tiled):
+    """uint8 docs take the tiled kernel from 65 query rows over docs of up to
+    128 tokens, and from 129 rows over up to 512 at d <= 128. There each code
+    is dequantised to fp16 before the MFMA, so besides the oracle check the
+    scores must equal, bit for bit, the fp16 path's on the fp16-dequantised
+    docs wherever that path also runs tiled (d <= 128)."""
+    from oracle import oracle_np
+
+    seed = 1300 + Lq + Ld + d
+    Q = sim((Lq, d), seed)
+    x = sim((B, Ld, d), seed + 1, torch.float32)
+    codes, s, m = fm.quantize_int8(x)
+    lengths = torch.randint(0, Ld + 2, (B,), generator=torch.Generator().manual_seed(seed), dtype=torch.int32)
+    lengths[0] = Ld
+    lengths[2] = 0
+    out = fm.flash_maxsim_int8(Q.to(DEV), codes.to(DEV), s.to(DEV), m.to(DEV), lengths.to(DEV))
+    _check(out, oracle_mod.maxsim_int8(to_np32(Q), codes.numpy(), to_np32(s), to_np32(m), lengths.numpy()))
+    dq = torch.from_numpy(oracle_np.dequantize_fp16_np(codes.numpy(), s.numpy(), m.numpy()))
+    if tiled and d <= 128:
+        ref16 = fm.flash_maxsim(Q.to(DEV), dq.to(DEV), lengths.to(DEV))
+        assert torch.equal(out, ref16)
+    _check(out, oracle_mod.maxsim(to_np32(Q), dq.float().numpy(), lengths.numpy())[0])

@@ -171,6 +171,40 @@ def test_int8_oracle_equals_dequantized(oracle_mod):
     np.testing.assert_array_equal(s8, s_ref)
 
 
+def _nearest_fp16(vals: np.ndarray, exact: np.ndarray) -> bool:
+    """True when every finite fp16 in vals is the one nearest exact (float64),
+    ties to an even significand, judged against both fp16 neighbours."""
+    fin = np.isfinite(vals)
+    g, e = vals[fin].astype(np.float64), exact[fin]
+    with np.errstate(over="ignore"):
+        up = np.nextafter(vals[fin], np.float16(np.inf)).astype(np.float64)
+        dn = np.nextafter(vals[fin], np.float16(-np.inf)).astype(np.float64)
+    err = np.abs(g - e)
+    if not (np.all(err <= np.abs(up - e)) and np.all(err <= np.abs(dn - e))):
+        return False
+    ties = (err == np.abs(up - e)) | (err == np.abs(dn - e))
+    return bool(np.all((vals[fin].view(np.uint16)[ties] & 1) == 0))
+
+
+def test_fp16_dequantisation_is_the_nearest_fp16():
+    """dequantize_fp16_np returns, for every token value, the fp16 nearest to
+    the exact code * scale + min; an fp16 multiply then add (two roundings, a
+    plausible slip) fails the same check on these values."""
+    rng = np.random.default_rng(21)
+    codes = rng.integers(0, 256, size=(64, 257)).astype(np.uint8)
+    scales = np.concatenate([rng.uniform(1e-4, 2e-2, 60), [6e-8, 1e-5, 3.0, 250.0]]).astype(np.float16)[:, None]
+    mins = np.concatenate([rng.uniform(-1.0, 0.5, 60), [-1e-6, 0.0, -300.0, 65000.0]]).astype(np.float16)[:, None]
+    got = oracle_np.dequantize_fp16_np(codes, scales, mins)
+    exact = codes.astype(np.float64) * scales.astype(np.float64) + mins.astype(np.float64)
+    fin = np.isfinite(got)
+    assert not fin.all() and fin.mean() > 0.9  # 65000 + 255 * 250 overflows fp16
+    assert np.all(np.abs(exact[~fin]) >= 65520)  # overflow only past the largest fp16 plus half an ulp
+    assert _nearest_fp16(got, exact)
+    with np.errstate(over="ignore"):
+        two_roundings = (codes.astype(np.float16) * scales).astype(np.float16) + mins
+    assert not _nearest_fp16(two_roundings, exact)
+
+
 # --------------------------------------------- torch on the CPU agrees -----
 
 def test_matches_torch_maxsim_naive(oracle_mod):
