@@ -297,6 +297,7 @@ int int8_impl(const void* Q, int64_t q_stride_l, const uint8_t* D, int64_t d_str
   const bool sm8 = ((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(mins)) & 7u) == 0;
   const bool rows16 = (d_stride_l & 15) == 0 && (tok_group || (d_stride_b & 15) == 0);
   a.vec = (rows16 && sm8 && (tok_group || ((sm_stride_b & 3) == 0 && (Ld & 3) == 0))) ? 1 : 0;
+  if (rows16 && aligned16(D)) a.vec |= 2;  // without bit 0: 16-byte code loads, per-tile scale loads
   hipStream_t s = static_cast<hipStream_t>(stream);
   const hipError_t e = tiled                   ? fmx::launch_tiled_fwd(fmx::KIND_U8, a, tp, false, s)
                        : plan_fwd(Lq, d).splitd ? fmx::launch_splitd_fwd(fmx::KIND_U8, a, false, s)

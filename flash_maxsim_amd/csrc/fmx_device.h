@@ -28,6 +28,7 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
 
 // Element kinds of the document operand.
 enum Kind : int { KIND_F16 = 0, KIND_BF16 = 1, KIND_U8 = 2 };
@@ -57,6 +58,9 @@ __device__ __forceinline__ u32x4_t ld16(rsrc_t r, uint32_t voff) {
 }
 __device__ __forceinline__ u32x2_t ld8(rsrc_t r, uint32_t voff) {
   return __builtin_amdgcn_raw_buffer_load_b64(r, voff, 0, 0);
+}
+__device__ __forceinline__ u32x3_t ld12(rsrc_t r, uint32_t voff) {
+  return __builtin_amdgcn_raw_buffer_load_b96(r, voff, 0, 0);
 }
 __device__ __forceinline__ uint32_t ld4(rsrc_t r, uint32_t voff) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0);

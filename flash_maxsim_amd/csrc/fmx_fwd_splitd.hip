@@ -364,7 +364,7 @@ hipError_t dispatch_flags(const FwdArgs& a, bool am, hipStream_t s) {
   const bool kmask = a.d != 32 * KSW * kSplitWaves;
   if constexpr (KIND == KIND_U8) {
     (void)am;
-    if (a.vec) {
+    if (a.vec & 1) {
       return kmask ? launch_one<KIND, NQB, KSW, true, false, true>(a, s)
                    : launch_one<KIND, NQB, KSW, false, false, true>(a, s);
     }

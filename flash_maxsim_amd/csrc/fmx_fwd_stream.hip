@@ -69,7 +69,8 @@ constexpr int stream_min_waves() {
 }
 
 // PD: ring depth other than stream_depth's (0: stream_depth's).
-template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX, bool VEC, int DOCS = 1, bool JOINT = false, int PD = 0>
+template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX, bool VEC, int DOCS = 1, bool JOINT = false, int PD = 0,
+          bool C16 = VEC>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(stream_min_waves<KIND, NQB, KS, VEC, DOCS>())))
 stream_fwd_kernel(FwdArgs a) {
   constexpr int NW = kStreamWaves, P = PD ? PD : stream_depth<KIND, NQB, KS>(), QROWS = NQB * 16;
@@ -213,7 +214,9 @@ stream_fwd_kernel(FwdArgs a) {
     r.s = past ? nul : (in1 ? s1 : s0);
     r.m = past ? nul : (in1 ? n1 : n0);
     r.rowb = dr0.rowb;
-    load_tile<KIND, KS, VEC, !GSM>(T, r, past ? 0 : (in1 ? sq - nt0 : sq), c, g, koff);
+    r.ss = in1 ? dr1.ss : dr0.ss;
+    r.sm = in1 ? dr1.sm : dr0.sm;
+    load_tile<KIND, KS, VEC, !GSM, C16>(T, r, past ? 0 : (in1 ? sq - nt0 : sq), c, g, koff);
   };
   // GSM: the scales and mins of a group of P = 4 tiles come with one dword
   // load per array (per doc of the workgroup) instead of two 8-byte loads per
@@ -477,7 +480,7 @@ __global__ void __launch_bounds__(256) sum_passes_kernel(FwdArgs a, int npass) {
   a.scores[qi * a.ss_n + b * a.ss_b] = s;
 }
 
-template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX, bool VEC = true>
+template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX, bool VEC = true, bool C16 = VEC>
 hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
   constexpr int QROWS = NQB * 16;
   const int npass = (a.Lq + QROWS - 1) / QROWS;
@@ -497,12 +500,13 @@ hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
         // tokens: 22.0 -> 19.3 us, 20000: 77.9 -> 65.5 us, a 64-token query
         // -20 %, 128-token docs -5 %); longer docs keep it (200 tokens: +4 %
         // with two tiles, config 4: +7.5 %).
-        hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2, false, 2>), grid, dim3(256), 0, s,
-                           a);
+        hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2, false, 2, C16>), grid, dim3(256), 0,
+                           s, a);
       } else if (GROUPS && sm_rows * 2 + 64 < ((int64_t)1 << 31)) {
         hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2, GROUPS>), grid, dim3(256), 0, s, a);
       } else {
-        hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2, false, 0, C16>), grid, dim3(256), 0,
+                           s, a);
       }
       return hipGetLastError();
     }
@@ -536,8 +540,8 @@ hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
     }
   }
   const int64_t grid = npass > 1 ? ((items + 7) / 8) * 8 * npass : items;
-  hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC>), dim3((unsigned)grid), dim3(256), 0, s,
-                     a);
+  hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 1, false, 0, C16>), dim3((unsigned)grid),
+                     dim3(256), 0, s, a);
   if (npass > 1) {
     hipLaunchKernelGGL(sum_passes_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, a, npass);
   }
@@ -548,8 +552,10 @@ template <int KIND, int NQB, int KS>
 hipError_t dispatch_flags(const FwdArgs& a, bool am, hipStream_t s) {
   if constexpr (KIND == KIND_U8) {
     (void)am;
-    return a.vec ? launch_one<KIND, NQB, KS, true, false, true>(a, s)
-                 : launch_one<KIND, NQB, KS, true, false, false>(a, s);
+    // FwdArgs::vec bit 0: the vector path; bit 1: 16-byte code rows only
+    if (a.vec & 1) return launch_one<KIND, NQB, KS, true, false, true>(a, s);
+    return (a.vec & 2) ? launch_one<KIND, NQB, KS, true, false, false, true>(a, s)
+                       : launch_one<KIND, NQB, KS, true, false, false, false>(a, s);
   } else {
     const bool kmask = a.d != 32 * KS;
     if (kmask) return am ? launch_one<KIND, NQB, KS, true, true>(a, s) : launch_one<KIND, NQB, KS, true, false>(a, s);

@@ -31,8 +31,9 @@ struct FwdArgs {
                               // (then sd_b and sm_b are unused), or null
   int64_t tok_rows;           // packed docs: token rows in D (reads are clamped to them)
   int shared_docs;            // doc row of (query qi, doc b) is b, else qi*B + b
-  int vec;                    // uint8 docs: 16-byte aligned code rows and scales/mins
-                              // readable 4 tokens per 8-byte load (compile-time path)
+  int vec;                    // uint8 docs, bit 0: 16-byte aligned code rows and scales/mins
+                              // readable 4 tokens per 8-byte load; bit 1: 16-byte aligned
+                              // code rows (compile-time paths)
 };
 
 // Backward of the forward with saved argmax (Nq queries, shared docs).

@@ -55,6 +55,8 @@ struct DocRes {
   rsrc_t d;       // token rows, num_records = len * row bytes
   rsrc_t s, m;    // uint8 docs: scales / mins of the doc
   uint32_t rowb;  // bytes per token row
+  uint32_t ss, sm;  // uint8 docs without VEC: byte offset (0 or 2) of the doc's first
+                    // scale / min in s / m, whose bases are rounded down to 4 bytes
 };
 
 // tok_group[drow], taken as wave-uniform (drow is): the buffer resources built
@@ -93,12 +95,27 @@ __device__ __forceinline__ DocRes make_doc_res(const FwdArgs& a, int64_t drow, i
   }
   const int64_t drows = len < avail ? len : avail;
   r.d = make_rsrc((const char*)a.D + (avail > 0 ? doc_elem0<true>(a, drow) * ESZ : 0), (uint32_t)drows * r.rowb);
+  r.ss = 0u;
+  r.sm = 0u;
   if constexpr (KIND == KIND_U8) {
     const int64_t sm0 = a.tok_group ? (avail > 0 ? 4 * tok_group_of(a, drow) : 0) : drow * a.sm_b;
     int64_t n = VEC ? (int64_t)((len + 3) & ~3) : (int64_t)len;
     if (n > avail) n = avail;
-    r.s = make_rsrc(a.scales + sm0, (uint32_t)n * 2u);
-    r.m = make_rsrc(a.mins + sm0, (uint32_t)n * 2u);
+    if constexpr (VEC) {
+      r.s = make_rsrc(a.scales + sm0, (uint32_t)n * 2u);
+      r.m = make_rsrc(a.mins + sm0, (uint32_t)n * 2u);
+    } else {
+      // 2-byte aligned rows: the resources start at the 4-byte boundary at or
+      // below the doc's first value and end at the one at or above its last
+      // (never a new page: pages are 4-byte multiples), so the aligned 12-byte
+      // loads of load_tile stay in range for every valid token.
+      const uintptr_t ps = reinterpret_cast<uintptr_t>(a.scales + sm0);
+      const uintptr_t pm = reinterpret_cast<uintptr_t>(a.mins + sm0);
+      r.ss = (uint32_t)(ps & 3u);
+      r.sm = (uint32_t)(pm & 3u);
+      r.s = make_rsrc(reinterpret_cast<const void*>(ps & ~(uintptr_t)3), ((uint32_t)n * 2u + r.ss + 3u) & ~3u);
+      r.m = make_rsrc(reinterpret_cast<const void*>(pm & ~(uintptr_t)3), ((uint32_t)n * 2u + r.sm + 3u) & ~3u);
+    }
   } else {
     r.s = r.d;
     r.m = r.d;
@@ -107,14 +124,16 @@ __device__ __forceinline__ DocRes make_doc_res(const FwdArgs& a, int64_t drow, i
 }
 
 // SM (uint8): also load the tile's scales and mins (else the caller fills T.s, T.m).
-template <int KIND, int KS, bool VEC, bool SM = true>
+// C16 (uint8 without VEC): code rows are 16-byte aligned, so codes still come
+// 16 bytes per load while the scales take the unaligned path.
+template <int KIND, int KS, bool VEC, bool SM = true, bool C16 = VEC>
 __device__ __forceinline__ void load_tile(Tile<KIND, KS>& T, const DocRes& r, int tile, int c, int g,
                                           const uint32_t (&koff)[KS]) {
   const uint32_t base = (uint32_t)(tile * 16 + c) * r.rowb;
   if constexpr (KIND == KIND_U8) {
 #pragma unroll
     for (int h = 0; h < KS / 2; ++h) {
-      if constexpr (VEC) {
+      if constexpr (VEC || C16) {
         T.v[h] = ld16(r.d, base + koff[2 * h]);
       } else {
         const u32x2_t lo = ld8(r.d, base + koff[2 * h]);
@@ -132,10 +151,11 @@ __device__ __forceinline__ void load_tile(Tile<KIND, KS>& T, const DocRes& r, in
       T.s = ld8(r.s, o);
       T.m = ld8(r.m, o);
     } else {
-      T.s[0] = (uint32_t)ld2(r.s, o) | ((uint32_t)ld2(r.s, o + 2) << 16);
-      T.s[1] = (uint32_t)ld2(r.s, o + 4) | ((uint32_t)ld2(r.s, o + 6) << 16);
-      T.m[0] = (uint32_t)ld2(r.m, o) | ((uint32_t)ld2(r.m, o + 2) << 16);
-      T.m[1] = (uint32_t)ld2(r.m, o + 4) | ((uint32_t)ld2(r.m, o + 6) << 16);
+      // the four values sit r.ss (r.sm) bytes into the 4-byte aligned 12 bytes
+      // at o: one load per array and two byte-funnel shifts
+      const u32x3_t s3 = ld12(r.s, o), m3 = ld12(r.m, o);
+      T.s = u32x2_t{__builtin_amdgcn_alignbyte(s3[1], s3[0], r.ss), __builtin_amdgcn_alignbyte(s3[2], s3[1], r.ss)};
+      T.m = u32x2_t{__builtin_amdgcn_alignbyte(m3[1], m3[0], r.sm), __builtin_amdgcn_alignbyte(m3[2], m3[1], r.sm)};
     }
   }
 }
