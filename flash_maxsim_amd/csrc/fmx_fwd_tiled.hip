@@ -726,12 +726,14 @@ bool tiled_fwd_applicable(int64_t Nq, int64_t Lq, int64_t Ld, int d) {
 // uint8 docs (single queries): the tiled kernel from 65 query rows over docs
 // of up to 128 tokens, and at d <= 128 from 129 rows (several streaming
 // passes) over docs of up to 512 tokens. 5000 docs of 77 tokens: 128 rows
-// 45.7 -> 31.4 us, 80 rows 43.2 -> 30.6, 256 rows 102.0 -> 42.9, d = 256
-// 130.4 -> 90.1; 128 rows over 64/96/128 tokens -21/-7/-6 %; 200/300/512
-// rows over 300 tokens -17/-6/-20 %. The streaming kernel stays faster for 64
-// rows over 77 tokens (24.7 against 29.3 us), 128 rows over 200 tokens (-5 %),
-// 512 rows over 1024 tokens (-8 %), 128 rows over 300 tokens at d = 256 (67.0
-// against 104.6 us) and any query of up to 64 rows over longer docs.
+// 35.6 -> 31.3 us, 80 rows 33.9 -> 30.4, 256 rows 92.8 -> 42.7, d = 256
+// 98.3 -> 90.3; 128 rows over 64/96/128 tokens 29.7 -> 23.3, 35.9 -> 33.1,
+// 39.7 -> 37.1 us; 2000 docs of 300 tokens under 200 rows 59.3 -> 49.0 us,
+// 301 tokens under 300 rows 85.4 -> 78.4 us, 1000 of 300 under 512 rows
+// -20 %. The streaming kernel stays faster for 64 rows over 77 tokens (24.7
+// against 29.3 us), 128 rows over 200 tokens (-5 %), 512 rows over 1024
+// tokens (-8 %), 128 rows over 300 tokens at d = 256 (67.0 against 104.6 us)
+// and any query of up to 64 rows over longer docs.
 bool tiled_u8_applicable(int64_t Lq, int64_t Ld, int d) {
   if (d < 1 || d > 256 || Lq <= 64) return false;
   if (Ld <= 128) return true;
