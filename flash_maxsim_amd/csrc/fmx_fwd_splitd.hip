@@ -29,7 +29,7 @@ constexpr int kSplitWaves = 8;
 // VEC: uint8 vector load path (FwdArgs::vec); true for fp16/bf16.
 // PERSIST (one query, one pass, no query gather): a fixed grid of resident
 // workgroups loads the query slice once and walks docs b, b + G, ...
-template <int KIND, int NQB, int KSW, bool KMASK, bool ARGMAX, bool VEC, bool PERSIST = false>
+template <int KIND, int NQB, int KSW, bool KMASK, bool ARGMAX, bool VEC, bool PERSIST = false, bool C16 = VEC>
 __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
   constexpr int NW = kSplitWaves, QROWS = NQB * 16;
   // Tiles in flight per wave: 2 when the query slice takes 128 VGPRs, which
@@ -193,9 +193,9 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int t = 0; t < KSW; ++t) acc[nb] = mfma16x16x32<BF>(af[t], qf[nb][t], acc[nb]);
     }
-    if constexpr (MODE == REFILL_ANY) load_tile<KIND, KSW, VEC, SM>(T, dr, tile + P, c, g, koff);
+    if constexpr (MODE == REFILL_ANY) load_tile<KIND, KSW, VEC, SM, C16>(T, dr, tile + P, c, g, koff);
     if constexpr (MODE == REFILL_IF) {
-      if (tile + P < ntiles) load_tile<KIND, KSW, VEC, SM>(T, dr, tile + P, c, g, koff);
+      if (tile + P < ntiles) load_tile<KIND, KSW, VEC, SM, C16>(T, dr, tile + P, c, g, koff);
     }
     // The first half of the query blocks finished first: store them, then
     // reduce the previous tile while the second half runs.
@@ -234,7 +234,7 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
     auto run = [&](auto sm_tag) __attribute__((always_inline)) {
       constexpr bool SM = decltype(sm_tag)::value;
 #pragma unroll
-      for (int s = 0; s < P; ++s) load_tile<KIND, KSW, VEC, SM>(buf[s], dr, s, c, g, koff);
+      for (int s = 0; s < P; ++s) load_tile<KIND, KSW, VEC, SM, C16>(buf[s], dr, s, c, g, koff);
       int i0 = 0;
       for (; i0 + P < ntiles; i0 += P) {
 #pragma unroll
@@ -256,7 +256,7 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
   } else {
 #pragma unroll
     for (int s = 0; s < P; ++s)
-      if (s < ntiles) load_tile<KIND, KSW, VEC>(buf[s], dr, s, c, g, koff);
+      if (s < ntiles) load_tile<KIND, KSW, VEC, true, C16>(buf[s], dr, s, c, g, koff);
     for (int i0 = 0; i0 < ntiles; i0 += P) {
 #pragma unroll
       for (int s = 0; s < P; ++s)
@@ -315,7 +315,7 @@ __global__ void __launch_bounds__(256) splitd_sum_passes_kernel(FwdArgs a, int n
   a.scores[qi * a.ss_n + b * a.ss_b] = s;
 }
 
-template <int KIND, int NQB, int KSW, bool KMASK, bool ARGMAX, bool VEC = true>
+template <int KIND, int NQB, int KSW, bool KMASK, bool ARGMAX, bool VEC = true, bool C16 = VEC>
 hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
   constexpr int QROWS = NQB * 16;
   const int npass = (a.Lq + QROWS - 1) / QROWS;
@@ -350,8 +350,8 @@ hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
   const int64_t U = (a.shared_docs && a.Nq > 1 ? a.Nq : 1) * (int64_t)npass;
   const int64_t nslots = a.shared_docs && a.Nq > 1 ? a.B : items;
   const int64_t grid = U > 1 ? ((nslots + 7) / 8) * 8 * U : items;
-  hipLaunchKernelGGL((splitd_fwd_kernel<KIND, NQB, KSW, KMASK, ARGMAX, VEC>), dim3((unsigned)grid), dim3(512), 0, s,
-                     a);
+  hipLaunchKernelGGL((splitd_fwd_kernel<KIND, NQB, KSW, KMASK, ARGMAX, VEC, false, C16>), dim3((unsigned)grid),
+                     dim3(512), 0, s, a);
   if (npass > 1) {
     hipLaunchKernelGGL(splitd_sum_passes_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, a,
                        npass);
@@ -367,6 +367,11 @@ hipError_t dispatch_flags(const FwdArgs& a, bool am, hipStream_t s) {
     if (a.vec & 1) {
       return kmask ? launch_one<KIND, NQB, KSW, true, false, true>(a, s)
                    : launch_one<KIND, NQB, KSW, false, false, true>(a, s);
+    }
+    // without the vector path: 16-byte code loads when the code rows allow (bit 1)
+    if (a.vec & 2) {
+      return kmask ? launch_one<KIND, NQB, KSW, true, false, false, true>(a, s)
+                   : launch_one<KIND, NQB, KSW, false, false, false, true>(a, s);
     }
     return kmask ? launch_one<KIND, NQB, KSW, true, false, false>(a, s)
                  : launch_one<KIND, NQB, KSW, false, false, false>(a, s);

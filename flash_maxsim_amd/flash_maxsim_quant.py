@@ -85,6 +85,15 @@ def dequantize_int8(D_uint8: torch.Tensor, scales: torch.Tensor, mins: torch.Ten
     return D_uint8.to(torch.float32) * scales.to(torch.float32) + mins.to(torch.float32)
 
 
+def _scale_rows(t: torch.Tensor, Ld: int) -> torch.Tensor:
+    """fp16 [B, Ld] scale or min rows as the kernels read them: t itself when
+    its tokens are adjacent and its rows at least Ld apart (any 2-byte
+    alignment), else a contiguous fp16 copy (reference :129-130 copies always)."""
+    if t.dtype == torch.float16 and t.stride(-1) == 1 and t.stride(0) >= Ld:
+        return t
+    return t.contiguous().half()
+
+
 def flash_maxsim_int8(
     Q: torch.Tensor,
     D_uint8: torch.Tensor,
@@ -113,8 +122,9 @@ def flash_maxsim_int8(
     lengths = _lengths(B, D_uint8.device, doc_lengths)
     Q = _prep(Q, torch.float16)
     D_uint8 = _prep(D_uint8, None)
-    scales = scales.contiguous().half()
-    mins = mins.contiguous().half()
+    scales, mins = _scale_rows(scales, Ld), _scale_rows(mins, Ld)
+    if scales.stride(0) != mins.stride(0):  # the kernel takes one row stride for both
+        scales, mins = scales.contiguous(), mins.contiguous()
     dev = _check_devices(Q, D_uint8, scales, mins, lengths)
     scores = torch.empty(B, device=dev, dtype=torch.float32)
     if B == 0:

@@ -106,10 +106,14 @@ int fmx_fwd_noalloc(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stri
  *
  *   Q        [Lq, d]   fp16, row stride q_stride_l
  *   D        [B, Ld, d] uint8 codes, strides (d_stride_b, d_stride_l, 1)
- *   scales   [B, Ld]   fp16, strides (sm_stride_b, 1)
- *   mins     [B, Ld]   fp16, strides (sm_stride_b, 1)
+ *   scales   [B, Ld]   fp16, strides (sm_stride_b, 1), 2-byte aligned
+ *   mins     [B, Ld]   fp16, strides (sm_stride_b, 1), 2-byte aligned
  *   lengths  [B]       int32, or NULL
  *   scores   [B]       fp32, contiguous
+ *
+ * Scale and min rows are read in aligned 4-byte words, so a read may touch
+ * the 2 bytes before a doc's first value or after its last (the same word,
+ * never another page); their contents do not matter.
  *
  * Replaces flash_maxsim/flash_maxsim_quant.py:135-141 (the launch in
  * flash_maxsim_int8) and _maxsim_int8_kernel (flash_maxsim_quant.py:40-98).

@@ -119,3 +119,31 @@ def test_int8_tiled_routes(oracle_mod, Lq, Ld, d, B, tiled):
         ref16 = fm.flash_maxsim(Q.to(DEV), dq.to(DEV), lengths.to(DEV))
         assert torch.equal(out, ref16)
     _check(out, oracle_mod.maxsim(to_np32(Q), dq.float().numpy(), lengths.numpy())[0])
+
+
+@pytest.mark.parametrize("Lq, Ld, d, B", [
+    (32, 301, 128, 7),    # stream, 16-byte code rows, scale rows 2-byte aligned
+    (32, 77, 96, 9),      # stream, two-tile ring
+    (128, 301, 512, 5),   # split-d, 16-byte code rows
+    (32, 77, 384, 6),
+    (32, 75, 1000, 4),    # split-d, 8-byte code rows (no 16-byte loads)
+])
+def test_int8_unaligned_scale_rows_routes(oracle_mod, Lq, Ld, d, B):
+    """Scale and min rows that start anywhere on a 2-byte boundary: views one
+    element into a wider store (read in place, NaN in the column before), so
+    doc b's first scale sits 2 bytes past a 4-byte boundary for some docs and
+    on one for others. The kernels read them with aligned 12-byte loads and
+    byte shifts, and keep 16-byte code loads where the code rows allow."""
+    seed = 1400 + Ld + d
+    Q = sim((Lq, d), seed)
+    x = sim((B, Ld, d), seed + 1, torch.float32)
+    codes, s, m = fm.quantize_int8(x)
+    lengths = torch.randint(0, Ld + 2, (B,), generator=torch.Generator().manual_seed(seed), dtype=torch.int32)
+    lengths[0] = Ld
+    lengths[1] = Ld - 1
+    s_store = torch.full((B, Ld + 1), float("nan"), dtype=torch.float16, device=DEV)
+    m_store = torch.full((B, Ld + 1), float("nan"), dtype=torch.float16, device=DEV)
+    s_store[:, 1:] = s[..., 0].to(DEV)
+    m_store[:, 1:] = m[..., 0].to(DEV)
+    out = fm.flash_maxsim_int8(Q.to(DEV), codes.to(DEV), s_store[:, 1:], m_store[:, 1:], lengths.to(DEV))
+    _check(out, oracle_mod.maxsim_int8(to_np32(Q), codes.numpy(), to_np32(s), to_np32(m), lengths.numpy()))
