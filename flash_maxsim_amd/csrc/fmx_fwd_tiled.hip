@@ -116,7 +116,8 @@ __device__ __forceinline__ void fold_rows(f32x4_t acc, int rowj, int len, bool t
 }
 
 // uint8 docs: a chunk of eight codes in registers with the fp16 bits of its
-// token's scale (low half) and min (high half).
+// token's scale (low half) and min (high half); a thread's chunks share one
+// token, whose scale and min only its chunk 0 holds.
 struct U8Chunk {
   u32x2_t codes;
   uint32_t sm;
@@ -288,18 +289,27 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
     return l < 0 ? 0 : (l > a.Ld ? a.Ld : l);
   };
   stage_t stage[CPT];
+  // Chunk k of this thread. fp16/bf16: chunks tid + k * (threads), so each
+  // load instruction of a wave covers 1 KB of consecutive chunks. uint8: the
+  // thread's CPT chunks are adjacent in one token row (CPR % CPT == 0), so it
+  // loads that row's scale and min once per tile instead of once per chunk
+  // (a wave still reads whole rows: 8 rows x 128 bytes at d = 128).
+  static_assert(!U8 || CPR % CPT == 0, "a uint8 thread's chunks share one token row");
+  auto chunk_of = [&](int k) __attribute__((always_inline)) { return U8 ? tid * CPT + k : tid + k * NW * 64; };
   auto load_tile_regs = [&](stage_t (&dst)[CPT], const TileRes& rd, int t) __attribute__((always_inline)) {
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      const int chunk = tid + k * NW * 64;
+      const int chunk = chunk_of(k);
       const int row = chunk / CPR, cc = chunk - (chunk / CPR) * CPR;
       const int e0 = cc * 8;
       uint32_t off = (uint32_t)(t * TJ + row) * rowb + (uint32_t)(e0 * ESZ);
       if (KMASK && e0 >= a.d) off = kOOB;
       if constexpr (U8) {
-        const uint32_t so = (uint32_t)(t * TJ + row) * 2u;
         dst[k].codes = ld8(rd.d, off);
-        dst[k].sm = (uint32_t)ld2(rd.s, so) | ((uint32_t)ld2(rd.m, so) << 16);
+        if (k == 0) {  // the row's scale and min, kept with chunk 0
+          const uint32_t so = (uint32_t)(t * TJ + row) * 2u;
+          dst[0].sm = (uint32_t)ld2(rd.s, so) | ((uint32_t)ld2(rd.m, so) << 16);
+        }
       } else {
         dst[k] = ld16(rd.d, off);
       }
@@ -310,11 +320,11 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
   auto store_tile_lds = [&](const stage_t (&src)[CPT], unsigned char* dst) __attribute__((always_inline)) {
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-      const int chunk = tid + k * NW * 64;
+      const int chunk = chunk_of(k);
       const int row = chunk / CPR, cc = chunk - (chunk / CPR) * CPR;
       u32x4_t v;
       if constexpr (U8) {
-        v = dequant8_f16(src[k].codes, src[k].sm);
+        v = dequant8_f16(src[k].codes, src[0].sm);
       } else {
         v = src[k];
       }
