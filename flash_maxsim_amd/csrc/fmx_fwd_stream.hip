@@ -199,8 +199,10 @@ stream_fwd_kernel(FwdArgs a) {
   // Sequence position -> (doc, tile of that doc); uniform over the wave.
   // Positions past the sequence read an empty range (zeros, no memory access).
   constexpr bool FIXED = !ARGMAX;  // fixed refill pattern (below)
-  constexpr bool GSM = U8 && VEC && P == 4;  // group scale loads (below)
-  static_assert(!GSM || P == 4, "group scale loads map 16 lanes per tile slot");
+  // group scale loads (below): the four-tile ring, and the two-tile ring of
+  // short doc pairs when one range covers both docs' scales (JOINT)
+  constexpr bool GSM = U8 && VEC && (P == 4 || (P == 2 && JOINT));
+  static_assert(!GSM || P == 4 || P == 2, "group scale loads map 16 lanes per tile slot");
   static_assert(!JOINT || DOCS == 2, "a joint scale range serves two-doc group loads");
   const rsrc_t nul = make_rsrc(a.D, 0u);
   auto seq_load = [&](Tile<KIND, KS>& T, int sq) {
@@ -256,7 +258,7 @@ stream_fwd_kernel(FwdArgs a) {
   }
   auto group_sm = [&](int ig, uint32_t& gs, uint32_t& gm) {
     const int sq = wave + NW * (ig + (lane >> 4));
-    const bool past = sq >= ntiles;
+    const bool past = sq >= ntiles || (lane >> 4) >= P;  // P = 2: lanes 32-63 idle
     const bool in1 = DOCS == 2 && sq >= nt0;
     const uint32_t off = (uint32_t)((in1 ? sq - nt0 : sq) * 32 + (lane & 7) * 4);
     if constexpr (JOINT) {
@@ -499,14 +501,22 @@ hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
       // 301-token docs 55.8 -> 38.5 us).
       constexpr bool GROUPS = VEC && stream_depth<KIND, NQB, KS>() == 4;  // group scale loads
       if (a.Ld <= 128) {
-        // Docs of up to 128 tokens: a two-tile ring (per-tile scale loads).
+        // Docs of up to 128 tokens: a two-tile ring.
         // The deeper ring's fixed refill pattern issues loads past a short
         // pair's tiles and its fill is paid per workgroup (5000 docs of 77
         // tokens: 22.0 -> 19.3 us, 20000: 77.9 -> 65.5 us, a 64-token query
         // -20 %, 128-token docs -5 %); longer docs keep it (200 tokens: +4 %
         // with two tiles, config 4: +7.5 %).
-        hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2, false, 2, C16>), grid, dim3(256), 0,
-                           s, a);
+        // With aligned scale rows one range covers both docs' scales and the
+        // ring's two tiles take their scales with one load per array (128-
+        // token docs 18.6 -> 17.3 us, 20000 docs of 76 tokens 44.6 -> 43.4 us).
+        if (VEC && sm_rows * 2 + 64 < ((int64_t)1 << 31)) {
+          hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2, VEC, 2, C16>), grid, dim3(256),
+                             0, s, a);
+        } else {
+          hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2, false, 2, C16>), grid, dim3(256),
+                             0, s, a);
+        }
       } else if (GROUPS && sm_rows * 2 + 64 < ((int64_t)1 << 31)) {
         hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2, GROUPS>), grid, dim3(256), 0, s, a);
       } else {
