@@ -140,6 +140,27 @@ __device__ __forceinline__ u32x4_t codes_to_f16_biased(u32x2_t raw) {
 // Bias of codes_to_f16_biased.
 constexpr float kCodeBias = 1024.0f;
 
+// Biased codes (codes_to_f16_biased) dequantised to fp16 as the reference's
+// int8 kernel dequantises before its dot product (flash_maxsim_quant.py:89):
+// code * scale + min rounded once (one v_pk_add_f16 removes the bias exactly,
+// one v_pk_fma_f16 rounds). sc_bits / mn_bits: fp16 bits in the low half.
+__device__ __forceinline__ u32x4_t dequant_biased_f16(u32x4_t h, uint32_t sc_bits, uint32_t mn_bits) {
+  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+  const h2_t sc = __builtin_bit_cast(h2_t, (sc_bits & 0xffffu) * 0x10001u);
+  const h2_t mn = __builtin_bit_cast(h2_t, (mn_bits & 0xffffu) * 0x10001u);
+  const h2_t bias = {(_Float16)kCodeBias, (_Float16)kCodeBias};
+  u32x4_t o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // bit_cast a copy: clang casts the first element for a vector subscript
+    const uint32_t hi = h[i];
+    const h2_t c = __builtin_bit_cast(h2_t, hi) - bias;
+    const uint32_t v = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, sc, mn));
+    o[i] = v;
+  }
+  return o;
+}
+
 __device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
 }

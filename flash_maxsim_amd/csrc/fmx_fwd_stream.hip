@@ -78,6 +78,15 @@ stream_fwd_kernel(FwdArgs a) {
   constexpr bool BF = KindInfo<KIND>::bf;
   constexpr bool U8 = KIND == KIND_U8;
   static_assert(DOCS == 1 || (DOCS == 2 && !ARGMAX), "two docs per workgroup: scores only");
+  // DQ: uint8 instances of eight query blocks (d <= 128, queries of more than
+  // 64 tokens) dequantise each tile's codes to fp16 before the MFMAs, as the
+  // reference's kernel does (flash_maxsim_quant.py:89), instead of applying
+  // the affine map to every result: that costs 2 packed ops per code pair
+  // (per k-step) against 2 VALU ops per result row and query block, so it
+  // pays where query blocks outnumber k-steps (Q[96,128] over 300-token docs
+  // 63.6 -> 59.7 us, 200-token docs -7 %, config 4's docs -2 %; at d = 256
+  // with four query blocks it lost 3.6 %).
+  constexpr bool DQ = U8 && NQB >= 8;
   __shared__ float red_m[DOCS][NW][QROWS];
   __shared__ int red_i[ARGMAX ? NW : 1][QROWS];
 
@@ -180,7 +189,7 @@ stream_fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int t = 0; t < KS; ++t) qf[nb][t] = qs[nb * KS + t][lane];
       qsum[nb] = 0.f;
-      if constexpr (U8) {
+      if constexpr (U8 && !DQ) {
         qsum[nb] = query_row_sum<KS>(qf[nb]);
       }
     }
@@ -201,7 +210,7 @@ stream_fwd_kernel(FwdArgs a) {
   constexpr bool FIXED = !ARGMAX;  // fixed refill pattern (below)
   // group scale loads (below): the four-tile ring, and the two-tile ring of
   // short doc pairs when one range covers both docs' scales (JOINT)
-  constexpr bool GSM = U8 && VEC && (P == 4 || (P == 2 && JOINT));
+  constexpr bool GSM = U8 && VEC && !DQ && (P == 4 || (P == 2 && JOINT));
   static_assert(!GSM || P == 4 || P == 2, "group scale loads map 16 lanes per tile slot");
   static_assert(!JOINT || DOCS == 2, "a joint scale range serves two-doc group loads");
   const rsrc_t nul = make_rsrc(a.D, 0u);
@@ -218,7 +227,7 @@ stream_fwd_kernel(FwdArgs a) {
     r.rowb = dr0.rowb;
     r.ss = in1 ? dr1.ss : dr0.ss;
     r.sm = in1 ? dr1.sm : dr0.sm;
-    load_tile<KIND, KS, VEC, !GSM, C16>(T, r, past ? 0 : (in1 ? sq - nt0 : sq), c, g, koff);
+    load_tile<KIND, KS, VEC, !GSM, C16, DQ>(T, r, past ? 0 : (in1 ? sq - nt0 : sq), c, g, koff);
   };
   // GSM: the scales and mins of a group of P = 4 tiles come with one dword
   // load per array (per doc of the workgroup) instead of two 8-byte loads per
@@ -314,12 +323,13 @@ stream_fwd_kernel(FwdArgs a) {
 #pragma unroll
     for (int t = 0; t < KS; ++t) {
       af[t] = tile_operand<KIND, KS>(T, t);
+      if constexpr (DQ) af[t] = dequant_biased_f16(af[t], T.s[0], T.m[0]);
       if constexpr (KMASK && !U8) {
         if (has_partial && t == tp) af[t] &= pmask;
       }
     }
     float sc[4], off[4];
-    if constexpr (U8) {
+    if constexpr (U8 && !DQ) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) tile_affine(T.s, T.m, r, sc[r], off[r]);
     }
@@ -344,7 +354,7 @@ stream_fwd_kernel(FwdArgs a) {
         f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int t = 0; t < KS; ++t) acc = mfma16x16x32<BF>(af[t], qf[nb][t], acc);
-        if constexpr (U8) {
+        if constexpr (U8 && !DQ) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[r] = fmaf(sc[r], acc[r], off[r] * qsum[nb]);
         }

@@ -134,21 +134,7 @@ struct TileRes {
 // fp16): code c is exact as fp16 (1024 + c, less 1024), then one fp16 fma
 // rounds c * scale + min once.
 __device__ __forceinline__ u32x4_t dequant8_f16(u32x2_t codes, uint32_t sm) {
-  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-  const h2_t sc = __builtin_bit_cast(h2_t, (sm & 0xffffu) * 0x10001u);
-  const h2_t mn = __builtin_bit_cast(h2_t, (sm >> 16) * 0x10001u);
-  const h2_t bias = {(_Float16)kCodeBias, (_Float16)kCodeBias};
-  const u32x4_t h = codes_to_f16_biased(codes);
-  u32x4_t o;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    // bit_cast a copy: clang casts the first element for a vector subscript
-    const uint32_t hi = h[i];
-    const h2_t c = __builtin_bit_cast(h2_t, hi) - bias;
-    const uint32_t v = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, sc, mn));
-    o[i] = v;
-  }
-  return o;
+  return dequant_biased_f16(codes_to_f16_biased(codes), sm, sm >> 16);
 }
 
 // Workgroup barrier once this wave's LDS accesses have completed, without

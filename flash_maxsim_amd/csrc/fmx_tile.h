@@ -126,7 +126,10 @@ __device__ __forceinline__ DocRes make_doc_res(const FwdArgs& a, int64_t drow, i
 // SM (uint8): also load the tile's scales and mins (else the caller fills T.s, T.m).
 // C16 (uint8 without VEC): code rows are 16-byte aligned, so codes still come
 // 16 bytes per load while the scales take the unaligned path.
-template <int KIND, int KS, bool VEC, bool SM = true, bool C16 = VEC>
+// ROWSM (uint8): T.s[0] / T.m[0] hold the scale / min of the lane's own token
+// row, tile*16 + c (for dequantising its A-fragment), instead of tokens
+// tile*16 + 4g .. +3 (its result rows).
+template <int KIND, int KS, bool VEC, bool SM = true, bool C16 = VEC, bool ROWSM = false>
 __device__ __forceinline__ void load_tile(Tile<KIND, KS>& T, const DocRes& r, int tile, int c, int g,
                                           const uint32_t (&koff)[KS]) {
   const uint32_t base = (uint32_t)(tile * 16 + c) * r.rowb;
@@ -145,7 +148,11 @@ __device__ __forceinline__ void load_tile(Tile<KIND, KS>& T, const DocRes& r, in
 #pragma unroll
     for (int t = 0; t < KS; ++t) T.v[t] = ld16(r.d, base + koff[t]);
   }
-  if constexpr (KIND == KIND_U8 && SM) {
+  if constexpr (KIND == KIND_U8 && SM && ROWSM) {
+    const uint32_t o = (uint32_t)(tile * 16 + c) * 2u;
+    T.s[0] = ld2(r.s, r.ss + o);
+    T.m[0] = ld2(r.m, r.sm + o);
+  } else if constexpr (KIND == KIND_U8 && SM) {
     const uint32_t o = (uint32_t)(tile * 16 + 4 * g) * 2u;
     if constexpr (VEC) {
       T.s = ld8(r.s, o);

@@ -4,14 +4,14 @@ Mirrors the reference module flash_maxsim/flash_maxsim_quant.py:
 quantize_int8 (:11-28), dequantize_int8 (:31-33) and flash_maxsim_int8
 (:105-142), with the same names, defaults, shapes and casts.
 
-flash_maxsim_int8 runs libflashmaxsim's uint8 kernels. The streaming and split-d
-kernels (queries of up to 64 tokens, or docs longer than 128 tokens) widen codes
-to fp16 exactly in registers and apply the per-token affine map to the fp32 MFMA
+flash_maxsim_int8 runs libflashmaxsim's uint8 kernels. Queries of up to 64
+tokens (and d > 256, and d > 128 over docs longer than 128 tokens) widen codes to
+fp16 exactly in registers and apply the per-token affine map to the fp32 MFMA
 result, S = scale * (Q . codes) + min * sum(Q), which equals Q . dequantize(codes)
-up to fp32 rounding. The tiled kernel (queries of 65+ tokens over docs of up to
-128 tokens, or of 129+ tokens over up to 512 at d <= 128) dequantises each code to
-fp16 (code * scale + min, rounded once) before the dot product, as the
-reference's kernel does; the two differ by under 1e-3 per score.
+up to fp32 rounding. Longer queries at d <= 128, and over docs of up to 128
+tokens at d <= 256, dequantise each code to fp16 (code * scale + min, rounded
+once) before the dot product, as the reference's kernel does; the two differ by
+under 1e-3 per score.
 """
 
 from __future__ import annotations

@@ -98,11 +98,12 @@ int fmx_fwd_noalloc(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stri
 /*
  * Fused uint8-dequant MaxSim forward: doc token j of doc b is
  * code * scales[b, j] + mins[b, j] (per-token affine, fp16 scale and min).
- * Queries of up to 64 tokens, and docs longer than 128 tokens (512 for
- * queries longer than 128 tokens at d <= 128), apply the affine map to the
- * fp32 dot product; longer queries over shorter docs round each dequantised
- * value to fp16 first, as the reference's kernel does (flash_maxsim_quant.py:
- * 89). The two differ by under 1e-3 per score at a few hundred query tokens.
+ * Queries of more than 64 tokens at d <= 128, and of more than 64 tokens over
+ * docs of up to 128 tokens at d <= 256, round each dequantised value to fp16
+ * before the dot product, as the reference's kernel does
+ * (flash_maxsim_quant.py:89); the others apply the affine map to the fp32
+ * dot product. The two differ by under 1e-3 per score at a few hundred query
+ * tokens.
  *
  *   Q        [Lq, d]   fp16, row stride q_stride_l
  *   D        [B, Ld, d] uint8 codes, strides (d_stride_b, d_stride_l, 1)
