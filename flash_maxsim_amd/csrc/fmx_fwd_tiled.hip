@@ -53,7 +53,7 @@ constexpr int kTiledNW = 8;                  // waves per workgroup
 // VGPRs) with 48 or 64 rows per wave at d <= 128: 192- and 256-row blocks
 // with twelve waves per CU where an eight-wave workgroup has eight (Nq = 8 x
 // 32 over 5000 docs 100.1 -> 92.7 us, Nq = 16 x 32 171.1 -> 163.9 us), and
-// with 16 rows per wave for blocks of at most 64 rows (tiled_fwd_plan).
+// with 16 or 32 rows per wave for blocks of at most 128 rows (tiled_fwd_plan).
 constexpr int tiled_wpc(int nw, int nb, int ks) { return nw == 4 ? 3 : (ks == 4 && nb <= 2) ? 2 : 1; }
 // waves per SIMD: a CU holds wpc workgroups of nw waves over its four SIMDs
 constexpr int tiled_waves_per_simd(int nw, int nb, int ks) { return tiled_wpc(nw, nb, ks) * nw / 4; }
@@ -674,6 +674,7 @@ hipError_t dispatch(const FwdArgs& a, const TiledPlan& p, bool am, hipStream_t s
     switch (p.nb) {
       case 4: return dispatch_flags<KIND, 4, 4, 4>(a, p, am, s);
       case 3: return dispatch_flags<KIND, 4, 3, 4>(a, p, am, s);
+      case 2: return dispatch_flags<KIND, 4, 2, 4>(a, p, am, s);
       case 1: return dispatch_flags<KIND, 4, 1, 4>(a, p, am, s);
       default: return hipErrorInvalidValue;
     }
@@ -809,18 +810,21 @@ TiledPlan tiled_fwd_plan(int64_t Nq, int64_t B, int64_t Lq, int d, int cus) {
       }
     }
   }
-  // At most 64 query rows in all (single queries of 33-64 tokens over short
-  // docs, at d <= 128): one 64-row block of four waves, three workgroups per
-  // CU, instead of an eight-wave 128-row block whose upper half is empty
-  // (5000 docs of 77 tokens: 64 rows 25.9 -> 21.0 us, 48 rows 25.6 -> 20.8
-  // us; 20000 docs 88.1 -> 71.4 us; 40 rows over 96 tokens 30.0 -> 24.6 us;
-  // d = 96 -12 %). The cost model above does not see the empty rows.
-  if (rows <= 64 && ks == 4) {
+  // At most 128 query rows in all at d <= 128 (single queries over short
+  // docs, a few batched queries): one block of four waves with 16 or 32 rows
+  // each, three workgroups per CU, instead of one eight-wave 128-row block
+  // per CU pair (5000 docs of 77 tokens: 64 rows 25.9 -> 21.0 us, 48 rows
+  // 25.6 -> 20.8, 128 rows 27.9 -> 21.5, 80 rows 27.1 -> 20.3; 20000 docs
+  // under 64 rows 88.1 -> 71.4 us; 96 rows over 150 tokens 42.6 -> 32.0 us;
+  // 4 x 32 and 2 x 64 rows over 300-token docs 83.3 -> 70.3 and 69.7 us;
+  // uint8 -5 %). The cost model above fits larger blocks and does not see
+  // the empty rows of a part-filled one.
+  if (rows <= 128 && ks == 4) {
     best = TiledPlan{};
     best.ks = 4;
     best.nw = 4;
-    best.nb = 1;
-    best.rows_per_block = 64;
+    best.nb = rows <= 64 ? 1 : 2;
+    best.rows_per_block = 64 * best.nb;
     best.nRB = 1;
     const int slots = (cus > 0 ? cus : 256) * tiled_wpc(4, 1, 4);
     int G = 8 * (slots / 8);
