@@ -716,10 +716,17 @@ hipError_t dispatch(const FwdArgs& a, const TiledPlan& p, bool am, hipStream_t s
 // 128 rows over 77-token docs 33.3 -> 25.3 us, at d = 96 45.8 -> 24.8 us; 48
 // and 64 rows over 77 tokens -5 % and -8 %; 96 rows over 150 tokens -7 %; 32
 // rows over 77 tokens and 64 over 150 stay faster streamed).
+// With four-wave blocks for up to 128 rows (tiled_fwd_plan) the tiled kernel
+// also takes single queries of 65-128 rows over docs of up to 512 tokens and
+// of 33-64 rows over up to 160 (5000 docs: 128 rows over 300 tokens 82.7 ->
+// 71.0 us, over 200 tokens 54.1 -> 41.3 us; 96 rows over 300 tokens 79.1 ->
+// 69.4 us; 64 rows over 150 tokens 37.7 -> 34.5 us); 33-64 rows over longer
+// docs stay streamed (64 rows over 300 tokens 69.2 against 70.4 us, 48 rows
+// 64.8 against 70.8, 40 rows over 200 tokens equal).
 bool tiled_fwd_applicable(int64_t Nq, int64_t Lq, int64_t Ld, int d) {
   if (d < 1 || d > 256) return false;
   if (Nq > 1 || Lq > 16 * stream_fwd_nqb(1 << 20, d)) return true;
-  return d <= 128 && ((Lq > 32 && Ld <= 96) || (Lq > 64 && Ld <= 160));
+  return d <= 128 && ((Lq > 32 && Ld <= 160) || (Lq > 64 && Ld <= 512));
 }
 
 // uint8 docs (single queries): the tiled kernel from 65 query rows over docs
