@@ -707,18 +707,15 @@ hipError_t dispatch(const FwdArgs& a, const TiledPlan& p, bool am, hipStream_t s
 // Batched queries over shared docs read each doc once here instead of once per
 // query (Nq = 2, Lq = 32: 93 against 103 us; Nq = 4: 96 against 198 us at
 // B = 5000, Ld = 300); a single query comes here once it needs more than one
-// pass of the streaming kernel (Lq = 200: 108 against 164 us), below that
-// the streaming kernel is faster (Lq = 96: 82 against 93 us), except over
-// short docs: the streaming kernel loads its query tile once per workgroup of
-// one or two docs, and from 33 query rows over docs of up to 96 tokens, or 65
-// rows over up to 160, that load outweighs what the persistent tiled
-// workgroups (query tile loaded once) lose elsewhere (d <= 128, 5000 docs:
-// 128 rows over 77-token docs 33.3 -> 25.3 us, at d = 96 45.8 -> 24.8 us; 48
-// and 64 rows over 77 tokens -5 % and -8 %; 96 rows over 150 tokens -7 %; 32
-// rows over 77 tokens and 64 over 150 stay faster streamed).
-// With four-wave blocks for up to 128 rows (tiled_fwd_plan) the tiled kernel
-// also takes single queries of 65-128 rows over docs of up to 512 tokens and
-// of 33-64 rows over up to 160 (5000 docs: 128 rows over 300 tokens 82.7 ->
+// pass of the streaming kernel (Lq = 200: 108 against 164 us). Below that the
+// streaming kernel loads its query tile once per workgroup of one or two
+// docs; with eight-wave blocks that load outweighed what the persistent tiled
+// workgroups lose elsewhere only over short docs (d <= 128, 5000 docs: 128
+// rows over 77-token docs 33.3 -> 25.3 us, at d = 96 45.8 -> 24.8 us; 32 rows
+// over 77 tokens stay faster streamed). With four-wave blocks for up to 128
+// rows (tiled_fwd_plan) the tiled kernel also takes single queries of 65-128
+// rows over docs of up to 512 tokens and of 33-64 rows over docs of up to 160
+// (5000 docs: 128 rows over 300 tokens 82.7 ->
 // 71.0 us, over 200 tokens 54.1 -> 41.3 us; 96 rows over 300 tokens 79.1 ->
 // 69.4 us; 64 rows over 150 tokens 37.7 -> 34.5 us); 33-64 rows over longer
 // docs stay streamed (64 rows over 300 tokens 69.2 against 70.4 us, 48 rows
