@@ -4,9 +4,9 @@ fmx_fwd picks, for single queries, the streaming kernel with one or two docs
 per workgroup or the tiled kernel by query rows, doc length and width, and
 pairs per-query docs. This file draws seeded shapes on both sides of those
 boundaries (query rows 32/33, 64/65, 128/129; doc lengths 96/97, 160/161,
-256/257; widths 64, 96, 128, 256) with ragged lengths, empty docs and odd
-doc counts, and checks every score against the float64 oracle (1e-2 absolute,
-the fp16 bar).
+256/257, 512/513; widths 64, 96, 128, 256) with ragged lengths, empty docs and
+odd doc counts, and checks every score against the float64 oracle (1e-2
+absolute, the fp16 bar).
 """
 
 from __future__ import annotations
@@ -175,3 +175,22 @@ def test_single_query_tiled_train_routes(oracle_mod, Lq, Ld, B):
     dQ_ref, dD_ref = oracle_mod.bwd(Qn, Dn, am.cpu().numpy(), g.numpy())
     np.testing.assert_allclose(Qg.grad.double().cpu().numpy(), dQ_ref, rtol=2e-3, atol=ATOL)
     np.testing.assert_allclose(Dg.grad.double().cpu().numpy(), dD_ref, rtol=2e-3, atol=ATOL)
+
+
+@pytest.mark.parametrize("Lq, Ld, d, dtype", [
+    (65, 512, 128, torch.float16),    # 65-128 rows up to 512 tokens: tiled, four-wave 128-row block
+    (128, 513, 128, torch.float16),   # past 512 tokens: streamed
+    (64, 160, 128, torch.bfloat16),   # 33-64 rows up to 160 tokens: tiled, four-wave 64-row block
+    (64, 161, 128, torch.float16),    # past 160 tokens: streamed
+    (33, 160, 96, torch.float16),     # masked width
+    (128, 512, 96, torch.bfloat16),
+    (100, 300, 128, torch.float16),
+])
+def test_single_query_four_wave_boundaries(oracle_mod, Lq, Ld, d, dtype):
+    B = 37
+    Q = sim((Lq, d), 1600 + Lq + Ld, dtype)
+    D = sim((B, Ld, d), 1601 + Lq + Ld, dtype)
+    lengths = torch.randint(0, Ld + 2, (B,), generator=torch.Generator().manual_seed(Lq * Ld), dtype=torch.int32)
+    lengths[0], lengths[1] = Ld, 0
+    out = fm.flash_maxsim(Q.to(DEV), D.to(DEV), lengths.to(DEV))
+    _check(out, oracle_mod.maxsim(to_np32(Q), to_np32(D), lengths.numpy())[0])
