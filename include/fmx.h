@@ -83,12 +83,17 @@ size_t fmx_fwd_workspace_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t Ld, in
  * workspace: the partial sums fmx_fwd keeps in its workspace (queries that
  * take several passes, queries straddling row blocks) go to a static device
  * array of FMX_NOALLOC_SCRATCH_BYTES on each GPU, held until the process
- * ends. A call whose fmx_fwd_workspace_bytes exceeds that fails with
- * FMX_ERR_UNSUPPORTED before any launch. The call allocates nothing (no
- * hipMalloc, no allocating library routine); its first call on a GPU looks up
- * that GPU's copy of the array. Every call on one GPU shares that GPU's array:
- * calls that overlap on one GPU (other streams, other threads) race, and must
- * be ordered by the caller. Nothing in the array needs to start at zero.
+ * ends. A call whose chosen kernels need more scratch than that fails with
+ * FMX_ERR_UNSUPPORTED before any launch; fmx_fwd_workspace_bytes bounds that
+ * need over every kernel route the sizes allow, so a call can succeed where
+ * that bound exceeds the limit, never the other way round. The call
+ * allocates nothing (no hipMalloc, no allocating library routine). The
+ * first call on a GPU that needs scratch looks up that GPU's copy of the
+ * array (hipGetSymbolAddress), so make that call outside stream capture;
+ * later calls may be captured into a HIP graph and replayed. Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (other
+ * streams, other threads) race, and must be ordered by the caller. Nothing in
+ * the array needs to start at zero.
  */
 int fmx_fwd_noalloc(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, const void* D,
                     int64_t d_stride_b, int64_t d_stride_l, const int32_t* lengths, float* scores,

@@ -133,8 +133,12 @@ def f32_to_f16_bits(x: float) -> int:
     return int(_load().oracle_f32_to_f16(float(x)))
 
 
-def bwd(Q, D, argmax, grad):
-    """(dQ [Lq, d], dD [B, Ld, d]) in float64 for the single-query argmax backward."""
+def bwd(Q, D, argmax, grad, want_dD=True):
+    """(dQ [Lq, d], dD [B, Ld, d]) in float64 for the single-query argmax backward.
+
+    With want_dD=False only dQ is formed (dD is None): the C function skips a
+    NULL output, so dQ of docs too large to hold dD for costs no B*Ld*d array.
+    """
     Q = _f32(Q)
     D = _f32(D)
     B, Ld, d = D.shape
@@ -142,7 +146,7 @@ def bwd(Q, D, argmax, grad):
     am = _i32(argmax).reshape(B, Lq)
     g = np.ascontiguousarray(np.asarray(grad, dtype=np.float64))
     dQ = np.empty((Lq, d), dtype=np.float64)
-    dD = np.empty((B, Ld, d), dtype=np.float64)
+    dD = np.empty((B, Ld, d), dtype=np.float64) if want_dD else None
     _load().oracle_bwd(_p(Q), _p(D), _p(am), _p(g), B, Lq, Ld, d, _p(dQ), _p(dD))
     return dQ, dD
 

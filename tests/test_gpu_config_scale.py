@@ -111,6 +111,101 @@ def test_config5_train_full_checks(oracle_mod):
     np.testing.assert_allclose(Dg.grad.double().cpu().numpy(), dD_ref, rtol=2e-3, atol=ATOL)
 
 
+def _config5_docs(B, Ld, d, seed):
+    """Config 5's docs built on the GPU from a seeded generator: N(0,1) rows,
+    L2-normalised, fp16 (the reference recipe, tests/test_flash_maxsim.py:6-9)."""
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    D = torch.empty(B, Ld, d, dtype=torch.float16, device=DEV)
+    for b0 in range(0, B, 250):
+        b1 = min(B, b0 + 250)
+        D[b0:b1] = torch.nn.functional.normalize(torch.randn(b1 - b0, Ld, d, generator=g, device=DEV), dim=-1)
+    return D
+
+
+def test_config5_full_size(oracle_mod):
+    """Config 5 at its workload size: flash_maxsim_train on Q[128,1024] x
+    D[1000,512,1024] fp16, loss = scores.sum() (reference
+    flash_maxsim.py:253-291, benchmarks/bench.py:110-122). The split-d forward
+    runs persistent here (one workgroup per CU walks docs b, b + G, ...), so
+    the sampled docs include the first and last of each walk step at 256
+    resident workgroups. Scores and the saved argmax on the sample; dQ over
+    all 1000 docs from the GPU's argmax (dQ-only oracle); dD on the sample."""
+    B, Lq, Ld, d = 1000, 128, 512, 1024
+    Q = sim((Lq, d), 51)
+    D = _config5_docs(B, Ld, d, 52)
+    Qg = Q.to(DEV).requires_grad_(True)
+    Dg = D.requires_grad_(True)
+    s = fm.flash_maxsim_train(Qg, Dg)
+    am = s.grad_fn.saved_tensors[2]  # [B, Lq] int32, kept alive past backward
+    s.sum().backward()
+    torch.cuda.synchronize()
+    pick = sorted(set(sample_docs(B, 16, 5)) | {0, 255, 256, 511, 512, 767, 768, 999})
+    Qn = to_np32(Q)
+    Dp = to_np32(D[pick])
+    ref, am_ref, best = oracle_mod.maxsim(Qn, Dp, want_argmax=True)
+    assert_scores(s[pick], ref[0])
+    am_all = am.cpu().numpy()
+    assert_argmax(torch.from_numpy(am_all[pick]), am_ref, best, Qn, Dp, d)
+    assert am_all.min() >= 0 and am_all.max() < Ld
+    # dQ over every doc: sum of the oracle's dQ over chunks of docs (additive in b)
+    dQ_ref = np.zeros((Lq, d))
+    for b0 in range(0, B, 100):
+        part, _ = oracle_mod.bwd(Qn, to_np32(D[b0:b0 + 100]), am_all[b0:b0 + 100], np.ones(100), want_dD=False)
+        dQ_ref += part
+    np.testing.assert_allclose(Qg.grad.double().cpu().numpy(), dQ_ref, rtol=2e-3, atol=ATOL)
+    _, dD_ref = oracle_mod.bwd(Qn, Dp, am_all[pick], np.ones(len(pick)))
+    np.testing.assert_allclose(Dg.grad[pick].double().cpu().numpy(), dD_ref, rtol=2e-3, atol=ATOL)
+
+
+@pytest.mark.parametrize("Lq, d, B, dtype, with_argmax", [
+    (128, 1024, 600, torch.float16, True),    # 132 KB of LDS: one workgroup per CU, up to 3 docs each
+    (128, 1024, 600, torch.float16, False),
+    (64, 512, 1300, torch.float16, True),     # 64 KB: two per CU, up to 3 docs each
+    (64, 512, 1300, torch.bfloat16, False),
+    (100, 1024, 700, torch.float16, False),   # masked query rows
+    (64, 768, 1300, torch.float16, True),     # masked k (24 of 32 k-steps per slice set)
+])
+def test_splitd_persistent_walk(oracle_mod, Lq, d, B, dtype, with_argmax):
+    """The split-d kernel's persistent form (one query in one pass of 64 rows
+    or more) with more docs than resident workgroups: each workgroup scores
+    several docs in turn, reusing its LDS row maxima and argmax, with empty
+    docs and tile-edge lengths in the later steps of the walk. Every doc is
+    checked against the oracle."""
+    Ld = 40
+    Q = sim((Lq, d), 2000 + Lq + d, dtype)
+    D = sim((B, Ld, d), 2001 + B, dtype)
+    lengths = torch.randint(1, Ld + 1, (B,), generator=torch.Generator().manual_seed(B + d), dtype=torch.int32)
+    for b, n in ((0, Ld), (255, 0), (256, 16), (257, 0), (300, 1), (511, 17), (512, 0), (513, Ld),
+                 (B - 2, 0), (B - 1, 15)):
+        lengths[b] = n
+    Qn, Dn, ln = to_np32(Q), to_np32(D), lengths.numpy()
+    if with_argmax:
+        from flash_maxsim_amd.flash_maxsim import _launch_fwd, _prep
+
+        out, am = _launch_fwd(_prep(Q.to(DEV), dtype)[None], _prep(D.to(DEV), dtype), lengths.to(DEV), 1, B, Lq,
+                              Ld, d, True, True)
+        ref, am_ref, best = oracle_mod.maxsim(Qn, Dn, ln, want_argmax=True)
+        assert_scores(out[0], ref[0])
+        assert_argmax(am, am_ref, best, Qn, Dn, d, ln)
+    else:
+        out = fm.flash_maxsim(Q.to(DEV), D.to(DEV), lengths.to(DEV))
+        assert_scores(out, oracle_mod.maxsim(Qn, Dn, ln)[0])
+
+
+def test_splitd_persistent_walk_int8(oracle_mod):
+    """uint8 docs on the persistent split-d form: 64 query rows at d = 512 over
+    1300 docs (several docs per resident workgroup)."""
+    B, Lq, Ld, d = 1300, 64, 40, 512
+    Q = sim((Lq, d), 2101)
+    x = sim((B, Ld, d), 2102, torch.float32)
+    codes, sc, mn = fm.quantize_int8(x)
+    lengths = torch.randint(0, Ld + 1, (B,), generator=torch.Generator().manual_seed(2103), dtype=torch.int32)
+    lengths[600], lengths[1299] = 0, Ld
+    out = fm.flash_maxsim_int8(Q.to(DEV), codes.to(DEV), sc.to(DEV), mn.to(DEV), lengths.to(DEV))
+    ref = oracle_mod.maxsim_int8(to_np32(Q), codes.numpy(), to_np32(sc), to_np32(mn), lengths.numpy())
+    assert_scores(out, ref)
+
+
 def test_train_many_dq_chunks(oracle_mod):
     """1000 docs at d = 128: the dQ gather runs its maximum of 64 doc chunks."""
     B, Lq, Ld, d = 1000, 32, 64, 128

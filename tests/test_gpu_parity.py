@@ -7,9 +7,11 @@ same fp16/bf16 values.
 
 Tolerances: scores within 1e-2 absolute of the oracle (north-star bar for
 fp16 inputs with fp32 accumulation). Argmax must equal the oracle's except at
-numerical ties: a mismatch is accepted only when the oracle's own similarity
-at the GPU's index is within TIE_TOL of the max. Gradients within 1e-2
-absolute (fp16/bf16 outputs).
+numerical ties (see assert_argmax: Higham's bound for the two similarities,
+and a cap on how many such ties one check may accept). Gradients (fp16
+outputs) within rtol 2e-3 + atol 1e-2 of the oracle's, computed from the
+GPU's accepted argmax; bf16 outputs within rtol 1e-2 + atol 2e-2, since bf16
+keeps 8 significant bits (half an ulp is 2^-8 = 3.9e-3 relative).
 """
 
 from __future__ import annotations
@@ -27,9 +29,25 @@ ATOL = 1e-2
 DEV = "cuda"
 
 
-def tie_tol(d: int) -> float:
-    # fp32 accumulation of d products of unit-norm rows: |error| <= ~d * 2^-24.
-    return 4.0 * d * 2.0**-24 + 1e-7
+U32 = 2.0**-24          # unit roundoff of fp32
+MFMA_MARGIN = 2.0       # the MFMA's internal rounding of its 32-term sums is not specified as
+                        # round-to-nearest: 2 allows a directed rounding at every step
+TIE_RATE = 5e-5         # accepted ties per (doc, query token) pair: about 5x the expected rate
+                        # of near-tie flips for random unit-norm rows at d = 1024 (~1e-5)
+TIE_FLOOR = 2           # ...but at least this many in one check
+
+
+def gamma(d: int) -> float:
+    """Higham's gamma_d = d*u / (1 - d*u): a d-term fp32 sum in any order is
+    within gamma_d * sum|terms| of the exact sum."""
+    return d * U32 / (1.0 - d * U32)
+
+
+def tie_tol(d: int, a_gpu: float, a_ref: float) -> float:
+    """Largest exact gap S(j_ref) - S(j_gpu) at which the GPU's fp32
+    similarities can still rank j_gpu first: the two fp32 sums are each within
+    gamma_d * sum_k |Q_qk D_jk| (a_gpu, a_ref) of their exact values."""
+    return MFMA_MARGIN * gamma(d) * (a_gpu + a_ref)
 
 
 def assert_scores(gpu: torch.Tensor, ref: np.ndarray, atol: float = ATOL):
@@ -44,20 +62,35 @@ def assert_scores(gpu: torch.Tensor, ref: np.ndarray, atol: float = ATOL):
 
 def assert_argmax(am_gpu: torch.Tensor, am_ref: np.ndarray, best_ref: np.ndarray, Q, D, d: int,
                   lengths=None):
-    """Bit-exact except at ties; returns the number of tie-accepted mismatches."""
+    """Bit-exact except at numerical ties; returns the number of tie-accepted
+    mismatches.
+
+    A GPU index j in place of the oracle's j* is accepted only when the
+    oracle's exact similarities satisfy S(j*) - S(j) <= tie_tol, and at most
+    max(TIE_FLOOR, TIE_RATE * pairs) such ties are accepted per check, so an
+    index bug that picks a near-max token systematically fails the count.
+    """
     g = am_gpu.cpu().numpy().reshape(am_ref.shape)
-    bad = np.argwhere(g != am_ref)
+    # an empty doc (every token masked, best = -inf) has no max to point at; the
+    # backward ignores its indices, so only docs with tokens are compared
+    bad = np.argwhere((g != am_ref) & (best_ref != -np.inf))
     Qn = np.asarray(Q, np.float64)
+    Qn = Qn if Qn.ndim == 3 else Qn[None]  # [Nq, Lq, d]; items run qi * B + b over shared docs
     Dn = np.asarray(D, np.float64)
     for item, q in bad:
-        j = g[item, q]
-        b = item % Dn.shape[0]
+        j, jr = int(g[item, q]), int(am_ref[item, q])
+        qi, b = divmod(int(item), Dn.shape[0])
+        qv = Qn[qi, q]
         n = Dn.shape[1] if lengths is None else min(max(int(lengths[b]), 0), Dn.shape[1])
         assert 0 <= j < max(n, 1), f"argmax {j} out of range at ({item}, {q})"
-        s = float(Qn[q] @ Dn[b, j])
-        assert abs(s - best_ref[item, q]) <= tie_tol(d), (
-            f"argmax mismatch at ({item}, {q}): gpu {j} (S={s:.9f}) vs oracle {am_ref[item, q]} "
-            f"(S={best_ref[item, q]:.9f})")
+        s = float(qv @ Dn[b, j])
+        tol = tie_tol(d, float(np.abs(qv * Dn[b, j]).sum()), float(np.abs(qv * Dn[b, jr]).sum()))
+        assert best_ref[item, q] - s <= tol, (
+            f"argmax mismatch at ({item}, {q}): gpu {j} (S={s:.9f}) vs oracle {jr} "
+            f"(S={best_ref[item, q]:.9f}), gap {best_ref[item, q] - s:.3e} > tie tolerance {tol:.3e}")
+    allowed = max(TIE_FLOOR, int(np.ceil(TIE_RATE * g.size)))
+    print(f"argmax: {len(bad)} tie-accepted of {g.size} pairs (at most {allowed})")
+    assert len(bad) <= allowed, f"{len(bad)} tie-accepted argmax mismatches in {g.size} pairs > {allowed}"
     return len(bad)
 
 
@@ -376,6 +409,13 @@ def test_sparse_varlen_large_d(oracle_mod):
 
 # --------------------------------------------------------------- training ----
 
+def grad_tol(dtype):
+    """(rtol, atol) for gradients stored in dtype: fp16 keeps 11 significant
+    bits (half an ulp is 2^-11 = 4.9e-4 relative), bf16 only 8 (2^-8 = 3.9e-3,
+    above the fp16 rtol of 2e-3)."""
+    return (1e-2, 2e-2) if dtype == torch.bfloat16 else (2e-3, ATOL)
+
+
 def run_train(oracle_mod, B, Lq, Ld, d, seed, dtype=torch.float16):
     Q = sim((Lq, d), seed, dtype)
     D = sim((B, Ld, d), seed + 1, dtype)
@@ -500,8 +540,9 @@ def test_tiled_bf16_and_argmax(oracle_mod):
     _, am = _launch_fwd(Q2[None], D2, None, 1, 6, 512, 100, 128, True, True)
     assert_argmax(am, am_ref, best, Qn, Dn, 128)
     dQ_ref, dD_ref = oracle_mod.bwd(Qn, Dn, am.cpu().numpy(), g.numpy())
-    np.testing.assert_allclose(dQ.double().cpu().numpy(), dQ_ref, rtol=1e-2, atol=2e-2)
-    np.testing.assert_allclose(dD.double().cpu().numpy(), dD_ref, rtol=1e-2, atol=2e-2)
+    rtol, atol = grad_tol(torch.bfloat16)
+    np.testing.assert_allclose(dQ.double().cpu().numpy(), dQ_ref, rtol=rtol, atol=atol)
+    np.testing.assert_allclose(dD.double().cpu().numpy(), dD_ref, rtol=rtol, atol=atol)
 
 
 @pytest.mark.parametrize("Nq, Lq, B, Ld, d, dtype", [
@@ -556,5 +597,6 @@ def test_tiled_four_wave_argmax(oracle_mod, Lq, Ld, d, dtype):
     _, am = _launch_fwd(Q2[None], D2, None, 1, B, Lq, Ld, d, True, True)
     assert_argmax(am, am_ref, best, Qn, Dn, d)
     dQ_ref, dD_ref = oracle_mod.bwd(Qn, Dn, am.cpu().numpy(), g.numpy())
-    np.testing.assert_allclose(dQ.double().cpu().numpy(), dQ_ref, rtol=1e-2, atol=2e-2)
-    np.testing.assert_allclose(dD.double().cpu().numpy(), dD_ref, rtol=1e-2, atol=2e-2)
+    rtol, atol = grad_tol(dtype)
+    np.testing.assert_allclose(dQ.double().cpu().numpy(), dQ_ref, rtol=rtol, atol=atol)
+    np.testing.assert_allclose(dD.double().cpu().numpy(), dD_ref, rtol=rtol, atol=atol)

@@ -127,6 +127,8 @@ def test_int8_tiled_routes(oracle_mod, Lq, Ld, d, B, tiled):
     (128, 301, 512, 5),   # split-d, 16-byte code rows
     (32, 77, 384, 6),
     (32, 75, 1000, 4),    # split-d, 8-byte code rows (no 16-byte loads)
+    (100, 77, 128, 6),    # tiled kernel (65+ query rows over docs of up to 128 tokens)
+    (96, 301, 128, 5),    # stream, eight query blocks: fp16 dequantisation of each tile
 ])
 def test_int8_unaligned_scale_rows_routes(oracle_mod, Lq, Ld, d, B):
     """Scale and min rows that start anywhere on a 2-byte boundary: views one
@@ -194,3 +196,53 @@ def test_single_query_four_wave_boundaries(oracle_mod, Lq, Ld, d, dtype):
     lengths[0], lengths[1] = Ld, 0
     out = fm.flash_maxsim(Q.to(DEV), D.to(DEV), lengths.to(DEV))
     _check(out, oracle_mod.maxsim(to_np32(Q), to_np32(D), lengths.numpy())[0])
+
+
+def test_int8_padding_route_difference_bounded(oracle_mod):
+    """The same uint8 docs padded to 128 tokens (tiled kernel: each value
+    rounded to fp16 before the dot product) and to 129 (streamed: the affine
+    map applied to the fp32 dot product), d = 256, 100 query tokens. Scores
+    are not padding-invariant. The 128-token scores must match the oracle on
+    the fp16-dequantised docs within Higham's bound of the fp32 sums (so the
+    route computes exactly that); the oracle's own fp16-vs-fp32 difference must
+    stay within the fp16 rounding bound sum_q max_j sum_k |Q_qk| (2^-11 |x_jk| +
+    2^-25); and the two routes' scores must differ by under 1e-3, the figure
+    the C header states."""
+    from oracle.oracle_np import dequantize_fp16_np, dequantize_np
+    from test_gpu_parity import MFMA_MARGIN, gamma
+
+    B, Lq, d = 40, 100, 256
+    Q = sim((Lq, d), 1700)
+    x = sim((B, 128, d), 1701, torch.float32)
+    codes, s, m = fm.quantize_int8(x)
+    lengths = torch.randint(1, 129, (B,), generator=torch.Generator().manual_seed(1702), dtype=torch.int32)
+    lengths[0] = 128
+    c129 = torch.zeros(B, 129, d, dtype=torch.uint8)
+    s129 = torch.ones(B, 129, 1, dtype=torch.float16)
+    m129 = torch.zeros(B, 129, 1, dtype=torch.float16)
+    c129[:, :128], s129[:, :128], m129[:, :128] = codes, s, m
+    Qd, ld = Q.to(DEV), lengths.to(DEV)
+    out128 = fm.flash_maxsim_int8(Qd, codes.to(DEV), s.to(DEV), m.to(DEV), ld).double().cpu().numpy()
+    out129 = fm.flash_maxsim_int8(Qd, c129.to(DEV), s129.to(DEV), m129.to(DEV), ld).double().cpu().numpy()
+    Qn, ln = to_np32(Q), lengths.numpy()
+    ref32 = oracle_mod.maxsim_int8(Qn, codes.numpy(), to_np32(s), to_np32(m), ln)
+    x16 = dequantize_fp16_np(codes.numpy(), s.numpy(), m.numpy()).astype(np.float32)
+    ref16, _, best16 = oracle_mod.maxsim(Qn, x16, ln, want_argmax=True)
+    ref16 = ref16[0]
+    assert np.abs(out128 - ref32).max() <= 1e-2 and np.abs(out129 - ref32).max() <= 1e-2
+    qa = np.abs(Qn.astype(np.float64))  # [Lq, d]
+    valid = np.arange(128)[None, :, None] < ln[:, None, None]
+
+    def per_score(per):  # [B, 128, Lq] bound per similarity -> [B] bound per score
+        return np.where(valid, per, 0.0).max(axis=1).sum(axis=1)
+
+    A16 = np.abs(x16.astype(np.float64)) @ qa.T  # [B, 128, Lq]: sum_k |Q_qk x16_jk|
+    # the similarities' bound, plus the fp32 sum of the Lq row maxima
+    tiled_bound = per_score(MFMA_MARGIN * gamma(d) * A16) + gamma(Lq) * np.abs(best16).sum(axis=1)
+    assert (np.abs(out128 - ref16) <= tiled_bound * 1.001).all()
+    A32 = np.abs(dequantize_np(codes.numpy(), s.numpy(), m.numpy()).astype(np.float64)) @ qa.T
+    rounding = per_score(2.0**-11 * A32 + 2.0**-25 * qa.sum(1)[None, None, :])
+    assert (np.abs(ref16 - ref32) <= rounding * 1.001).all()
+    diff = np.abs(out128 - out129)
+    print(f"uint8 padding 128 vs 129: max |diff| {diff.max():.3e}; fp16 rounding bound {rounding.min():.3e}")
+    assert diff.max() < 1e-3

@@ -5,8 +5,9 @@ doc_lengths) against the oracle (scores, the argmax the forward saves, and
 the backward formula applied to that argmax: oracle.bwd per query, summed over
 queries for dD), and against float64 autograd through the reference's own
 naive MaxSim (maxsim_naive) on the CPU, which fixes what an empty doc
-contributes (no gradient). Tolerances as in test_gpu_parity.py: scores and
-gradients within 1e-2 of the oracle.
+contributes (no gradient). Tolerances as in test_gpu_parity.py: scores
+within 1e-2 of the oracle, the saved argmax exact up to its tie rule,
+gradients within rtol 2e-3 + atol 1e-2.
 """
 
 from __future__ import annotations
@@ -18,6 +19,7 @@ import torch
 import flash_maxsim_amd as fm
 from conftest import sim, to_np32
 from flash_maxsim_amd.flash_maxsim import _launch_fwd, _prep
+from test_gpu_parity import assert_argmax
 
 pytestmark = pytest.mark.gpu
 
@@ -73,6 +75,8 @@ def test_train_with_doc_lengths(oracle_mod, B, Lq, Ld, d):
     for b in range(B):
         if clamped[b] > 0:
             assert (am[0, b] < clamped[b]).all()
+    _, am_ref, best = oracle_mod.maxsim(Qn, Dn, lengths.numpy(), want_argmax=True)
+    assert_argmax(torch.from_numpy(am), am_ref, best, Qn, Dn, d, lengths.numpy())
     dQ_ref, dD_ref = reference_grads(oracle_mod, Qn, Dn, am, g.numpy(), clamped)
     np.testing.assert_allclose(Qg.grad.double().cpu().numpy(), dQ_ref[0], rtol=2e-3, atol=ATOL)
     np.testing.assert_allclose(Dg.grad.double().cpu().numpy(), dD_ref, rtol=2e-3, atol=ATOL)
@@ -105,6 +109,8 @@ def test_train_batched(oracle_mod, Nq, B, Lq, Ld, d):
     np.testing.assert_array_equal(s.detach().cpu().numpy(),
                                   fm.flash_maxsim_batched(Q.to(DEV), D.to(DEV), lengths.to(DEV)).cpu().numpy())
     am = saved_argmax(Qn, Dn, lengths.numpy())
+    _, am_ref, best = oracle_mod.maxsim(Qn, Dn, lengths.numpy(), want_argmax=True)
+    assert_argmax(torch.from_numpy(am), am_ref, best, Qn, Dn, d, lengths.numpy())
     dQ_ref, dD_ref = reference_grads(oracle_mod, Qn, Dn, am, g.numpy(), lengths.numpy())
     np.testing.assert_allclose(Qg.grad.double().cpu().numpy(), dQ_ref, rtol=2e-3, atol=ATOL)
     np.testing.assert_allclose(Dg.grad.double().cpu().numpy(), dD_ref, rtol=2e-3, atol=ATOL)

@@ -266,6 +266,13 @@ def test_bwd_matches_autograd(oracle_mod):
     dQ, dD = oracle_mod.bwd(Q.float().numpy(), D.float().numpy(), am, g.numpy())
     np.testing.assert_allclose(dQ, Qr.grad.numpy(), rtol=0, atol=1e-6)
     np.testing.assert_allclose(dD, Dr.grad.numpy(), rtol=0, atol=1e-6)
+    # dQ alone (no dD array) is the same dQ, and dQ is additive over chunks of docs
+    dQ_only, none = oracle_mod.bwd(Q.float().numpy(), D.float().numpy(), am, g.numpy(), want_dD=False)
+    assert none is None
+    np.testing.assert_array_equal(dQ_only, dQ)
+    parts = [oracle_mod.bwd(Q.float().numpy(), D[b0:b0 + 2].float().numpy(), am[b0:b0 + 2], g[b0:b0 + 2].numpy(),
+                            want_dD=False)[0] for b0 in (0, 2, 4)]
+    np.testing.assert_allclose(parts[0] + parts[1] + parts[2], dQ, rtol=0, atol=1e-12)
 
 
 # ------------------------------------------------ planted mistakes ------

@@ -58,3 +58,38 @@ def test_noalloc_matches_fmx_fwd(name):
         run(lib, Q, D, lengths, got, Nq, B, Lq, Ld, d, shared, True)
         torch.cuda.synchronize()
         assert torch.equal(got, want), f"{name} call {i}: max diff {(got - want).abs().max().item()}"
+
+
+def test_noalloc_graph_replays():
+    """fmx_fwd_noalloc captured into a HIP graph on a side stream (after an
+    eager call on the device has looked up the scratch address), replayed three
+    times with eager work between the replays, among it an eager noalloc call
+    on other inputs that rewrites the shared scratch: each replay must give
+    fmx_fwd's scores bit for bit."""
+    lib = _lib.load()
+    Nq, Lq, B, Ld, d, shared = 3, 700, 30, 90, 128, 1  # tiled kernel, queries straddling row blocks
+    Q = sim((Nq, Lq, d), 501).to(DEV)
+    D = sim((B, Ld, d), 502).to(DEV)
+    lengths = torch.randint(0, Ld + 4, (B,), generator=torch.Generator().manual_seed(503), dtype=torch.int32).to(DEV)
+    want = torch.empty(Nq, B, device=DEV)
+    run(lib, Q, D, lengths, want, Nq, B, Lq, Ld, d, shared, False)
+    Q2 = sim((2, 650, d), 504).to(DEV)
+    other = torch.empty(2, B, device=DEV)
+    run(lib, Q2, D, lengths, other, 2, B, 650, Ld, d, shared, True)  # eager: looks up the scratch
+    torch.cuda.synchronize()
+    got = torch.full((Nq, B), -7.0, device=DEV)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        run(lib, Q, D, lengths, got, Nq, B, Lq, Ld, d, shared, True)
+    torch.cuda.synchronize()
+    for r in range(3):
+        got.fill_(-7.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay {r}: max diff {(got - want).abs().max().item()}"
+        again = torch.empty(2, B, device=DEV)
+        run(lib, Q2, D, lengths, again, 2, B, 650, Ld, d, shared, True)  # eager work in between
+        torch.cuda.synchronize()
+        assert torch.equal(again, other)
