@@ -26,13 +26,14 @@
 namespace fmx {
 namespace {
 
-// Inverse of ord_of for numbers (NaN maps back to a canonical NaN, -0 to +0).
+// Inverse of ord_bits for numbers (NaN maps back to a canonical NaN, -0 to +0).
 __device__ __forceinline__ float float_of(uint32_t o) {
   return __builtin_bit_cast(float, (o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
 }
 
-__device__ __forceinline__ uint32_t ord_of(float f) {
-  uint32_t u = __builtin_bit_cast(uint32_t, f);
+// Float bits to an unsigned integer in float order: every NaN to the maximum
+// (NaN ranks first), -0 to +0's value.
+__device__ __forceinline__ uint32_t ord_bits(uint32_t u) {
   if ((u & 0x7fffffffu) > 0x7f800000u) return 0xffffffffu;  // NaN ranks first
   if (u == 0x80000000u) u = 0u;                                // -0 ties with +0
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
@@ -42,6 +43,12 @@ constexpr int kTopkThreads = 1024;
 constexpr int kTopkMaxK = 8192;                  // FMX_MAX_TOPK
 constexpr int kTopkCountK = 1024;                // ranked by counting up to this many keys
 constexpr int kTopkC = kTopkThreads * 16;       // keys per chunk (16 per thread)
+// A row of up to kTopkSmallN keys with k <= kTopkSmallK is selected by one
+// 512-thread workgroup on the raw scores (select_small_row): two waves per
+// SIMD, each step's latency hidden by the other wave.
+constexpr int kTopkSmallThreads = 512;
+constexpr int kTopkSmallN = kTopkSmallThreads * 16;
+constexpr int kTopkSmallK = 128;
 
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ int dpp_or0(int v) {
@@ -62,16 +69,17 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
   return v;
 }
 
+template <int NT>
 __device__ __forceinline__ int block_exclusive_scan(int v, int* wave_tot, int* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int inc = wave_incl_scan(v);
   if (lane == 63) wave_tot[wave] = inc;
   __syncthreads();
   if (wave == 0) {
-    const int t = lane < kTopkThreads / 64 ? wave_tot[lane] : 0;
+    const int t = lane < NT / 64 ? wave_tot[lane] : 0;
     const int ti = wave_incl_scan(t);
-    if (lane < kTopkThreads / 64) wave_tot[lane] = ti - t;  // exclusive wave offsets
-    if (lane == kTopkThreads / 64 - 1) *total = ti;
+    if (lane < NT / 64) wave_tot[lane] = ti - t;  // exclusive wave offsets
+    if (lane == NT / 64 - 1) *total = ti;
   }
   __syncthreads();
   return wave_tot[wave] + inc - v;
@@ -110,9 +118,13 @@ __device__ __forceinline__ void wave_minmax_u32(uint32_t& mn, uint32_t& mx) {
 // least `want` maxima sit in the bin (of a 256-bin histogram over the 8 bits
 // below the maxima's common prefix) that holds the want-th largest maximum or
 // above it, so at least `want` keys reach that bin's lower edge. 0 when fewer
-// than `want` threads hold keys.
+// than `want` threads hold keys. The largest maximum goes to *bmax.
+// PRECLEARED: hist was zeroed before the call (no clearing pass), every wave
+// scans the histogram itself (no broadcast of the bin), and the caller passes
+// a barrier before it rewrites hist, wlo or whi (none at the end).
+template <int NT, bool PRECLEARED = false>
 __device__ __forceinline__ uint32_t maxima_bound(uint32_t m, int want, uint32_t* hist, uint64_t* wlo, uint64_t* whi,
-                                                 int* bc) {
+                                                 int* bc, uint32_t* bmax = nullptr) {
   const int tid = threadIdx.x, lane = tid & 63;
   uint32_t mn = m == 0u ? 0xffffffffu : m, mx = m;
   wave_minmax_u32(mn, mx);
@@ -123,17 +135,39 @@ __device__ __forceinline__ uint32_t maxima_bound(uint32_t m, int want, uint32_t*
   __syncthreads();
   mn = 0xffffffffu;
   mx = 0u;
-  for (int w = 0; w < kTopkThreads / 64; ++w) {
+  for (int w = 0; w < NT / 64; ++w) {
     mn = (uint32_t)wlo[w] < mn ? (uint32_t)wlo[w] : mn;
     mx = (uint32_t)whi[w] > mx ? (uint32_t)whi[w] : mx;
   }
+  if (bmax) *bmax = mx;
   if (mx == 0u) return 0u;  // uniform: no barrier skipped by some threads only
   const int hb = mn == mx ? 8 : 32 - __builtin_clz(mn ^ mx);  // the maxima agree above bit hb
   const int sh = hb < 8 ? 0 : hb - 8;
-  if (tid < 256) hist[tid] = 0u;
-  __syncthreads();
+  if constexpr (!PRECLEARED) {
+    if (tid < 256) hist[tid] = 0u;
+    __syncthreads();
+  }
   if (m != 0u) atomicAdd(&hist[(m >> sh) & 255u], 1u);
   __syncthreads();
+  const uint32_t hi = sh + 8 >= 32 ? 0u : (mx >> (sh + 8)) << (sh + 8);
+  if constexpr (PRECLEARED) {
+    // every wave scans the histogram itself: no broadcast, no further barrier
+    uint32_t h[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) h[j] = hist[4 * lane + j];
+    const int incl = wave_incl_scan((int)(h[0] + h[1] + h[2] + h[3]));
+    uint32_t above = (uint32_t)(__builtin_amdgcn_readlane(incl, 63) - incl);
+    int found = -1;
+#pragma unroll
+    for (int j = 3; j >= 0; --j) {
+      if (above < (uint32_t)want && (uint32_t)want <= above + h[j]) found = 4 * lane + j;
+      above += h[j];
+    }
+    const uint64_t who = __builtin_amdgcn_ballot_w64(found >= 0);  // one lane at most
+    if (who == 0u) return 0u;
+    const int bin = __builtin_amdgcn_readlane(found, __builtin_ctzll(who));
+    return hi | ((uint32_t)bin << sh);
+  }
   if (tid < 64) {
     // lane l holds bins 4l .. 4l+3; maxima in higher bins = total - inclusive prefix
     uint32_t h[4];
@@ -152,30 +186,40 @@ __device__ __forceinline__ uint32_t maxima_bound(uint32_t m, int want, uint32_t*
   const int bin = bc[0];
   __syncthreads();  // bc, hist, wlo and whi are rewritten later
   if (bin < 0) return 0u;
-  const uint32_t hi = sh + 8 >= 32 ? 0u : (mx >> (sh + 8)) << (sh + 8);
   return hi | ((uint32_t)bin << sh);
 }
 
 // Ranks the nsel distinct keys of sel[] (rank = keys greater) and writes the
 // best k: values and indices best first (values given) or this chunk's k keys
-// to keys_out. G lanes of one wave share a key's count, splitting the list.
-__device__ __forceinline__ void rank_and_write(const uint64_t* sel, int nsel, int k, const float* scores_row,
+// to keys_out. G lanes of one wave share a key's count, each comparing it
+// against its share of the list in batches of eight 16-byte pairs whose LDS
+// reads are all in flight before the first compare. The list is first padded
+// with zero keys to a whole number of batches (0 is below every real key, so
+// padding never counts); nsel <= kTopkCountK keeps the padded list inside sel.
+template <int NT>
+__device__ __forceinline__ void rank_and_write(uint64_t* sel, int nsel, int k, const float* scores_row,
                                                float* values_row, int64_t* indices_row, uint64_t* keys_chunk) {
   int G = 1;
-  while (G < 64 && 2 * G * nsel <= kTopkThreads) G *= 2;
+  while (2 * G <= 64 && 2 * G * nsel <= NT) G *= 2;  // the groups of G lanes cover nsel in one pass
+  const int span = 16 * G;  // keys one batch covers over the G lanes
+  const int padded = (nsel + span - 1) / span * span;
   const int tid = threadIdx.x, part = tid & (G - 1);
-  for (int j = tid / G; j < nsel; j += kTopkThreads / G) {  // all G lanes of a group share j
+  for (int t = nsel + tid; t < padded; t += NT) sel[t] = 0;
+  __syncthreads();
+  const ulonglong2* pairs = reinterpret_cast<const ulonglong2*>(sel);
+  for (int j = tid / G; j < nsel; j += NT / G) {  // all G lanes of a group share j
     const uint64_t kv = sel[j];
     int cnt = 0;
-    for (int p = part; 2 * p < nsel; p += G) {
-      if (2 * p + 1 < nsel) {
-        const ulonglong2 y = *reinterpret_cast<const ulonglong2*>(sel + 2 * p);
-        cnt += (y.x > kv) + (y.y > kv);
-      } else {
-        cnt += sel[2 * p] > kv;
-      }
+    for (int p0 = part; 2 * p0 < padded; p0 += 8 * G) {
+      ulonglong2 y[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) y[u] = pairs[p0 + u * G];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) cnt += (int)(y[u].x > kv) + (int)(y[u].y > kv);
     }
-    for (int o = 1; o < G; o <<= 1) cnt += __shfl_xor(cnt, o);
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1)
+      if (o < G) cnt += __shfl_xor(cnt, o);
     if (part == 0 && cnt < k) {
       if (values_row) {
         const int64_t idx = (int64_t)(uint32_t)~(uint32_t)kv;  // a real key: a valid index of the row
@@ -192,46 +236,193 @@ __device__ __forceinline__ void rank_and_write(const uint64_t* sel, int nsel, in
   }
 }
 
+// Selection of one row's k <= kTopkSmallK best scores by the small
+// instance, on the raw float bits (slots past the row become -inf): no
+// per-key order keys are formed. Each thread's largest score (a NaN-propagating
+// maximum, so a NaN anywhere in the row is seen), a bound from those maxima
+// (maxima_bound), then candidates and their rank by counting with G lanes
+// per candidate. Every step is branch-free VALU arithmetic on the sign of a
+// float difference, with +inf taken as the largest finite float (inf - inf
+// would be a NaN): x >= T is the clear sign bit of x - T' (T' = T, or -0 for
+// T = +0, so that -0 - T' = +0), and y > x the set sign bit of x - y (x and
+// y with -0 made +0; the exact difference's sign survives rounding). Values
+// that compare equal this way (+inf and the largest float included) collide
+// in the rank and send the row to the exact path.
+// Candidates are packed by one wave scan and one LDS atomic per wave; a lane
+// writes every slot, non-candidates to a spare entry of its own. The rank
+// buffer holds -inf past the candidates (x - (-inf) is +inf: never counted).
+// Returns false, uniformly and after a barrier, when the row holds a NaN, the
+// bound is -inf, there are more than kTopkCountK candidates, or two
+// candidates of equal value fall inside the top k (the rank then cannot order
+// them by index): the exact path runs instead.
+template <int NT, int E>
+__device__ bool select_small_row(uint32_t (&raw)[E], int left, int k, float* vrow, int64_t* irow,
+                                 uint32_t* hist, uint64_t* wmin, uint64_t* wmax, int* bcast, uint32_t* nsel_lds) {
+  constexpr int SPARE = kTopkCountK + 64;  // one spare entry per lane
+  __shared__ __attribute__((aligned(16))) float rel[SPARE];
+  __shared__ uint64_t pr[SPARE];  // index << 32 | score bits
+  __shared__ int rk[kTopkCountK];
+  __shared__ uint32_t slot[kTopkSmallK];
+  __shared__ int flag[2];  // [0]: a NaN in the row, [1]: equal values inside the top k
+  const int tid = threadIdx.x, lane = tid & 63;
+#pragma unroll
+  for (int t = tid; t < kTopkCountK; t += NT) rel[t] = -__builtin_inff();
+  if (tid < 256) hist[tid] = 0u;
+  if (tid < kTopkSmallK) slot[tid] = 0u;
+  if (tid < 2) flag[tid] = 0;
+  // (the LDS set-up above overlaps the loads; the first use of a score is here)
+  // slots past the row become -inf (the exact path masks them by index)
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (e * NT + tid >= left) raw[e] = 0xff800000u;
+  const int want = left < k ? left : k;
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int e = 0; e < E; ++e) m = __builtin_elementwise_maximum(m, __builtin_bit_cast(float, raw[e]));
+  if (__builtin_amdgcn_ballot_w64(m != m) != 0 && lane == 0) flag[0] = 1;
+  // a thread without any key of the row holds no maximum (0)
+  const uint32_t mo = tid < left ? ord_bits(__builtin_bit_cast(uint32_t, m)) : 0u;
+  const uint32_t tau = maxima_bound<NT, true>(mo, want, hist, wmin, wmax, bcast);
+  // Keys whose order reaches the bound are the scores >= T. A bound at or
+  // below the order of -inf would admit the -inf that stands in for slots
+  // past the row: such rows take the exact path.
+  if (tau <= 0x007fffffu) return false;  // uniform
+  constexpr float kBig = 3.40282347e38f;  // the largest finite float
+  const float T = __builtin_fminf(float_of(tau), kBig);
+  const float Tm = T == 0.f ? -0.f : T;
+  uint32_t out = 0u;  // slots that are not candidates
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    out += __builtin_bit_cast(uint32_t, __builtin_fminf(__builtin_bit_cast(float, raw[e]), kBig) - Tm) >> 31;
+  const int cnt = E - (int)out;
+  const int inc = wave_incl_scan(cnt);
+  uint32_t base = 0u;
+  if (lane == 63) base = atomicAdd(nsel_lds, (uint32_t)inc);
+  uint32_t pos = __builtin_amdgcn_readlane(base, 63) + (uint32_t)(inc - cnt);
+  const uint32_t spare = kTopkCountK + lane;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float x = __builtin_fminf(__builtin_bit_cast(float, raw[e]), kBig);
+    const uint32_t no = __builtin_bit_cast(uint32_t, x - Tm) >> 31;
+    const uint32_t p = pos < (uint32_t)(kTopkCountK - 1) ? pos : (uint32_t)(kTopkCountK - 1);
+    const uint32_t a = no ? spare : p;  // branch-free: non-candidates write a spare entry
+    pr[a] = ((uint64_t)(uint32_t)(e * NT + tid) << 32) | raw[e];
+    rel[a] = x + 0.f;  // -0 becomes +0
+    pos += 1u - no;
+  }
+  __syncthreads();
+  const int nc = (int)*nsel_lds;
+  if (flag[0] != 0 || nc > kTopkCountK || nc < want) return false;
+
+  constexpr int RB = 4;  // 16-byte reads per lane per batch
+  int G = 1;
+  while (2 * G <= 64 && 2 * G * nc <= NT) G *= 2;  // the groups of G lanes cover nc in one pass
+  const int span = 4 * RB * G;
+  const int padded = (nc + span - 1) / span * span;  // <= kTopkCountK: 4 * RB * G divides it
+  const int part = tid & (G - 1);
+  const f32x4_t* r4 = reinterpret_cast<const f32x4_t*>(rel);
+  for (int j = tid / G; j < nc; j += NT / G) {  // all G lanes of a group share j
+    const float xj = rel[j];
+    uint32_t c = 0u;
+    for (int q0 = part; 4 * q0 < padded; q0 += RB * G) {
+      f32x4_t y[RB];
+#pragma unroll
+      for (int u = 0; u < RB; ++u) y[u] = r4[q0 + u * G];
+#pragma unroll
+      for (int u = 0; u < RB; ++u)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) c += __builtin_bit_cast(uint32_t, xj - y[u][v]) >> 31;
+    }
+    int cc = (int)c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1)
+      if (o < G) cc += __shfl_xor(cc, o);
+    if (part == 0) {
+      rk[j] = cc;
+      if (cc < k && atomicAdd(&slot[cc], 1u) != 0u) flag[1] = 1;
+    }
+  }
+  __syncthreads();
+  if (flag[1] != 0) return false;
+  for (int t = tid; t < nc; t += NT) {
+    const int r = rk[t];
+    if (r < k) {
+      const uint64_t v = pr[t];
+      vrow[r] = __builtin_bit_cast(float, (uint32_t)v);  // the input's own bits (-0 stays -0)
+      irow[r] = (int64_t)(v >> 32);
+    }
+  }
+  return true;
+}
+
 // grid (chunks, rows). Level 0 (keys_in == null): row r's chunk c covers
 // indices [c*C, c*C + C) of scores[r, :n]. Otherwise keys_in[r, :n] (0 = no key).
 // Output: the chunk's k best keys to keys_out[r, c*k ...] (0-padded when the
 // chunk holds fewer), or, at the last level, values and indices, best first.
 // kTopkE: keys per thread (the chunk is 1024 * kTopkE keys); MAXK: capacity of
 // the selection buffer, kTopkCountK or kTopkMaxK (k above kTopkCountK).
-template <int kTopkE, int MAXK>
-__global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* scores, int64_t s_stride,
+template <int NT, int kTopkE, int MAXK, bool SMALL = false>
+__global__ void __launch_bounds__(NT) topk_level_kernel(const float* scores, int64_t s_stride,
                                                                  const uint64_t* keys_in, int64_t n, int k,
                                                                  uint64_t* keys_out, float* values,
                                                                  int64_t* indices, int64_t o_stride) {
   __shared__ uint32_t hist[256];
   __shared__ __attribute__((aligned(16))) uint64_t sel[MAXK];
-  __shared__ int wave_tot[kTopkThreads / 64];
-  __shared__ uint64_t wmin[kTopkThreads / 64], wmax[kTopkThreads / 64];
+  __shared__ int wave_tot[NT / 64];
+  __shared__ uint64_t wmin[NT / 64], wmax[NT / 64];
   __shared__ int bcast[4];
+  __shared__ uint32_t nsel_lds;  // candidates packed so far (cleared before the first barrier)
   const int64_t row = blockIdx.y;
-  const int64_t c0 = (int64_t)blockIdx.x * (kTopkThreads * kTopkE);
+  const int64_t c0 = (int64_t)blockIdx.x * (NT * kTopkE);
   const int tid = threadIdx.x;
+  if (tid == 0) nsel_lds = 0u;
 
+  // Every load is issued unconditionally, through a buffer resource over the
+  // chunk (reads past the row return 0 without touching memory, then count as
+  // no key), so all of a thread's loads are in flight together at one
+  // instruction each; a load under a per-key branch waited for each in turn.
+  const int64_t left64 = n - c0;
+  const int left = left64 < (int64_t)NT * kTopkE ? (int)left64 : NT * kTopkE;  // keys of this chunk
   uint64_t key[kTopkE];
   int valid = 0;
+  if (keys_in) {
+    const rsrc_t r = make_rsrc(keys_in + row * n + c0, (uint32_t)left * 8u);
 #pragma unroll
-  for (int e = 0; e < kTopkE; ++e) {
-    const int64_t i = c0 + (int64_t)e * kTopkThreads + tid;
-    uint64_t kv = 0;
-    if (i < n) kv = keys_in ? keys_in[row * n + i]
-                            : (((uint64_t)ord_of(scores[row * s_stride + i]) << 32) | (uint32_t)~(uint32_t)i);
-    key[e] = kv;
-    valid += kv != 0;
+    for (int e = 0; e < kTopkE; ++e) {
+      const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, (uint32_t)(tid + e * NT) * 8u, 0, 0);
+      key[e] = ((uint64_t)v[1] << 32) | v[0];
+    }
+#pragma unroll
+    for (int e = 0; e < kTopkE; ++e) valid += key[e] != 0;
+  } else {
+    const rsrc_t r = make_rsrc(scores + row * s_stride + c0, (uint32_t)left * 4u);
+    uint32_t raw[kTopkE];
+#pragma unroll
+    for (int e = 0; e < kTopkE; ++e)  // constant offsets fold into the instructions' offset fields
+      raw[e] = __builtin_amdgcn_raw_buffer_load_b32(r, (uint32_t)(tid + e * NT) * 4u, 0, 0);
+    if constexpr (SMALL) {
+      // the small instances run single-chunk rows at the last level only
+      if (select_small_row<NT, kTopkE>(raw, left, k, values + row * o_stride, indices + row * o_stride, hist,
+                                       wmin, wmax, bcast, &nsel_lds))
+        return;
+      __syncthreads();  // the exact path below packs its candidates again
+      if (tid == 0) nsel_lds = 0u;
+    }
+    const uint32_t nidx = ~(uint32_t)(c0 + tid);  // ~index of key 0; key e: nidx - e * NT
+#pragma unroll
+    for (int e = 0; e < kTopkE; ++e) {
+      const uint64_t kv = ((uint64_t)ord_bits(raw[e]) << 32) | (nidx - (uint32_t)(e * NT));
+      key[e] = e * NT + tid < left ? kv : 0;
+    }
   }
   // keys present in this chunk (0-keys are padding from an earlier level; at
   // level 0 every index below n is a key, none of them 0, so no count is needed)
   int total;
   if (!keys_in) {
-    const int64_t left = n - c0;
-    total = left < (int64_t)kTopkThreads * kTopkE ? (int)left : kTopkThreads * kTopkE;
+    total = left;
   } else {
     int* tot = &bcast[3];
-    block_exclusive_scan(valid, wave_tot, tot);
+    block_exclusive_scan<NT>(valid, wave_tot, tot);
     total = *tot;
   }
   const int want = total < k ? total : k;
@@ -250,18 +441,27 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* s
       const uint32_t h = (uint32_t)(key[e] >> 32);
       if (key[e] != 0 && h > m) m = h;
     }
-    const uint32_t tau = maxima_bound(m, want, hist, wmin, wmax, bcast);
+    const uint32_t tau = maxima_bound<NT>(m, want, hist, wmin, wmax, bcast);
     int c = 0;
 #pragma unroll
     for (int e = 0; e < kTopkE; ++e) c += key[e] != 0 && (uint32_t)(key[e] >> 32) >= tau;
-    int pos = block_exclusive_scan(c, wave_tot, &bcast[3]);
-    const int nc = bcast[3];
-    if (nc <= kTopkCountK) {  // uniform
+    // Each wave reserves its candidates' slots with one LDS atomic (slot order
+    // does not matter: ranking orders by key), one barrier instead of a block scan.
+    const int inc = wave_incl_scan(c);
+    int base = 0;
+    if ((tid & 63) == 63) base = (int)atomicAdd(&nsel_lds, (uint32_t)inc);
+    int pos = __builtin_amdgcn_readlane(base, 63) + inc - c;
 #pragma unroll
-      for (int e = 0; e < kTopkE; ++e)
-        if (key[e] != 0 && (uint32_t)(key[e] >> 32) >= tau) sel[pos++] = key[e];
-      __syncthreads();
-      rank_and_write(sel, nc, want, values ? scores + row * s_stride : nullptr,
+    for (int e = 0; e < kTopkE; ++e) {
+      if (key[e] != 0 && (uint32_t)(key[e] >> 32) >= tau) {
+        if (pos < kTopkCountK) sel[pos] = key[e];
+        ++pos;
+      }
+    }
+    __syncthreads();
+    const int nc = (int)nsel_lds;
+    if (nc <= kTopkCountK) {  // uniform
+      rank_and_write<NT>(sel, nc, want, values ? scores + row * s_stride : nullptr,
                      values ? values + row * o_stride : nullptr, values ? indices + row * o_stride : nullptr,
                      values ? nullptr : keys_out + row * nout + (int64_t)blockIdx.x * k);
       return;
@@ -296,7 +496,7 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* s
     __syncthreads();
     hmn = (uint32_t)wmin[0];
     hmx = (uint32_t)wmax[0];
-    for (int w = 1; w < kTopkThreads / 64; ++w) {
+    for (int w = 1; w < NT / 64; ++w) {
       hmn = (uint32_t)wmin[w] < hmn ? (uint32_t)wmin[w] : hmn;
       hmx = (uint32_t)wmax[w] > hmx ? (uint32_t)wmax[w] : hmx;
     }
@@ -328,7 +528,7 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* s
       __syncthreads();
       mn = wmin[0];
       mx = wmax[0];
-      for (int w = 1; w < kTopkThreads / 64; ++w) {
+      for (int w = 1; w < NT / 64; ++w) {
         mn = wmin[w] < mn ? wmin[w] : mn;
         mx = wmax[w] > mx ? wmax[w] : mx;
       }
@@ -388,7 +588,7 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* s
     mine += kv != 0 && want > 0 && (shift == 64 ? true : (kv >> shift) >= prefix);
   }
   int nsel;
-  int pos = block_exclusive_scan(mine, wave_tot, &bcast[3]);
+  int pos = block_exclusive_scan<NT>(mine, wave_tot, &bcast[3]);
   nsel = bcast[3];
 #pragma unroll
   for (int e = 0; e < kTopkE; ++e) {
@@ -402,7 +602,7 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* s
   __syncthreads();
 
   if (values && (MAXK <= kTopkCountK || nsel <= kTopkCountK)) {
-    rank_and_write(sel, nsel, k, scores + row * s_stride, values + row * o_stride, indices + row * o_stride,
+    rank_and_write<NT>(sel, nsel, k, scores + row * s_stride, values + row * o_stride, indices + row * o_stride,
                    nullptr);
   } else if (values) {
     // More keys than ranking by counting handles in time (O(n^2)): a bitonic
@@ -411,11 +611,11 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* s
     if constexpr (MAXK > kTopkCountK) {
       int np = 1;
       while (np < nsel) np <<= 1;
-      for (int t = nsel + tid; t < np; t += kTopkThreads) sel[t] = 0;
+      for (int t = nsel + tid; t < np; t += NT) sel[t] = 0;
       __syncthreads();
       for (int size = 2; size <= np; size <<= 1) {
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
-          for (int i = tid; i < np / 2; i += kTopkThreads) {
+          for (int i = tid; i < np / 2; i += NT) {
             const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
             const bool desc = (lo & size) == 0;  // every merge of the last size is descending
             const uint64_t x = sel[lo], y = sel[hi];
@@ -428,7 +628,7 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* s
         }
       }
       const float* scores_row = scores + row * s_stride;
-      for (int t = tid; t < nsel && t < k; t += kTopkThreads) {
+      for (int t = tid; t < nsel && t < k; t += NT) {
         const uint64_t kv = sel[t];
         const int64_t idx = (int64_t)(uint32_t)~(uint32_t)kv;
         float v = float_of((uint32_t)(kv >> 32));
@@ -438,7 +638,7 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* s
       }
     }
   } else {
-    for (int t = tid; t < k; t += kTopkThreads)
+    for (int t = tid; t < k; t += NT)
       keys_out[row * nout + (int64_t)blockIdx.x * k + t] = t < nsel ? sel[t] : 0;
   }
 }
@@ -455,11 +655,24 @@ hipError_t run_levels(const TopkArgs& a, hipStream_t s) {
     if (chunks > 0x7fffffff || a.Nq > 65535) return hipErrorInvalidValue;
     uint64_t* out = last ? nullptr : bufs[which];
     // a single chunk holds no more keys per thread than the row needs
-    auto kern = n <= 4 * kTopkThreads ? topk_level_kernel<4, MAXK>
-              : n <= 8 * kTopkThreads ? topk_level_kernel<8, MAXK> : topk_level_kernel<16, MAXK>;
-    hipLaunchKernelGGL(kern, dim3((unsigned)chunks, (unsigned)a.Nq), dim3(kTopkThreads), 0, s, a.scores,
-                       a.s_stride, in, n, a.k, out, last ? a.values : nullptr, last ? a.indices : nullptr,
-                       a.o_stride);
+    bool small = false;
+    if constexpr (MAXK == kTopkCountK) small = last && n <= kTopkSmallN && a.k <= kTopkSmallK;
+    if (small) {
+      if constexpr (MAXK == kTopkCountK) {
+        constexpr int T = kTopkSmallThreads;
+        auto kern = n <= 8 * T ? topk_level_kernel<T, 8, MAXK, true>
+                  : n <= 10 * T ? topk_level_kernel<T, 10, MAXK, true>
+                  : n <= 12 * T ? topk_level_kernel<T, 12, MAXK, true> : topk_level_kernel<T, 16, MAXK, true>;
+        hipLaunchKernelGGL(kern, dim3(1u, (unsigned)a.Nq), dim3(T), 0, s, a.scores, a.s_stride, in, n, a.k,
+                           nullptr, a.values, a.indices, a.o_stride);
+      }
+    } else {
+      constexpr int T = kTopkThreads;
+      auto kern = n <= 4 * T ? topk_level_kernel<T, 4, MAXK>
+                : n <= 8 * T ? topk_level_kernel<T, 8, MAXK> : topk_level_kernel<T, 16, MAXK>;
+      hipLaunchKernelGGL(kern, dim3((unsigned)chunks, (unsigned)a.Nq), dim3(T), 0, s, a.scores, a.s_stride, in, n,
+                         a.k, out, last ? a.values : nullptr, last ? a.indices : nullptr, a.o_stride);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || last) return e;
     in = out;

@@ -61,6 +61,59 @@ def test_topk_one_dim_and_strided_rows(oracle_mod):
         fm.topk_scores(t, 3001)
 
 
+def small_row_scores(kind, seed, shape, k):
+    """Rows for the 512-thread selection of up to 8192 scores with k <= 128,
+    which works on the raw floats and falls back to the exact path for NaN,
+    a bound at -inf, or equal values inside the top k."""
+    g = np.random.default_rng(seed)
+    s = g.standard_normal(shape).astype(np.float32)
+    B = shape[-1]
+    rows = s.reshape(-1, B)
+    if kind == "neg_zero_top":      # the best score is -0.0 (its bits must survive), the rest negative
+        rows[:] = -np.abs(rows) - 1e-3
+        rows[:, B // 2] = -0.0
+    elif kind == "zero_at_k":       # k - 1 positive scores, then +0 and -0 below them
+        rows[:] = -np.abs(rows) - 1.0
+        top = g.permutation(B)[: k + 1]
+        rows[:, top[: k - 1]] = np.arange(1, k, dtype=np.float32)[None, :]
+        rows[:, top[k - 1]] = 0.0
+        if k < B:
+            rows[:, top[k]] = -0.0
+    elif kind == "inf_top":         # one +inf (taken as the largest float inside the fast path)
+        rows[:, B // 3] = np.inf
+    elif kind == "two_inf":         # equal values inside the top k: the exact path
+        rows[:, B // 3] = np.inf
+        rows[:, (2 * B) // 3] = np.inf
+    elif kind == "neg_inf_heavy":   # most docs empty: the bound reaches -inf
+        rows[:, : (B * 19) // 20] = -np.inf
+    elif kind == "denormal":        # subnormal scores
+        rows[:] = rows * np.float32(1e-39)
+    elif kind == "ties_outside":    # exact ties everywhere below a distinct top k
+        rows[:] = np.round(rows * 4) / 4 - 10.0
+        top = g.permutation(B)[:k]
+        rows[:, top] = 10.0 + np.arange(k, dtype=np.float32)[None, :] * 0.5
+    elif kind == "ties_inside":     # exact ties inside the top k: the exact path
+        rows[:] = np.round(rows * 4) / 4
+    elif kind == "nan":             # a NaN ranks first: the exact path
+        rows[:, B // 5] = np.nan
+    return s
+
+
+@pytest.mark.parametrize("kind", ["normal", "neg_zero_top", "zero_at_k", "inf_top", "two_inf",
+                                  "neg_inf_heavy", "denormal", "ties_outside", "ties_inside", "nan"])
+@pytest.mark.parametrize("Nq, B, k", [
+    (1, 5000, 100), (3, 5000, 128), (1, 1, 1), (1, 7, 7), (2, 300, 10), (1, 511, 64), (1, 512, 128),
+    (1, 4096, 1), (1, 4097, 33), (2, 5120, 128), (1, 6144, 100), (1, 8192, 128),
+])
+def test_topk_small_rows(oracle_mod, kind, Nq, B, k):
+    """Rows of up to 8192 scores with k <= 128 (the selection after a
+    single-query scoring call): exactly the oracle's selection, value bits
+    included, whichever path each row takes."""
+    s = small_row_scores(kind, 7 * B + k, (Nq, B), k)
+    got = fm.topk_scores(torch.from_numpy(s).to(DEV), k)
+    assert_same_selection(got, oracle_mod.topk(s, k))
+
+
 def test_topk_all_equal_and_all_nan(oracle_mod):
     s = np.full((2, 4500), 0.5, np.float32)
     s[1] = np.nan
