@@ -11,7 +11,10 @@ Configs (the driver's line is the default, c1):
   c1_rot     the same with four distinct copies of D (1.5 GB) used in turn,
              so no step finds its docs in the 256 MB last-level cache
   c1_1000    config 1 at B = 1000 (its parity size)
-  c1_topk    config 1 followed by top-100 selection
+  c1_topk    config 1 followed by top-100 selection (flash_maxsim_topk, one call)
+  c1_torch_topk  config 1 followed by torch.topk(scores, 100): what callers do today
+  c1_floor   config 1 followed by a one-element fill kernel: the cost of any
+             dependent launch after scoring
   c2         config 2, visual: Q[1024,128] x D[1000,1024,128]
   c3         config 3, batched: Q[100,32,128] x D[5000,300,128], shared docs
   c3_pq      batched with per-query docs (shared_docs=False):
@@ -128,7 +131,7 @@ def build(name: str, rotate: int, doc_align: int = 4) -> Workload:
     dev = "cuda"
     f16 = torch.float16
 
-    if name in ("c1", "c1_rot", "c1_1000", "c1_topk"):
+    if name in ("c1", "c1_rot", "c1_1000", "c1_topk", "c1_torch_topk", "c1_floor"):
         B = 1000 if name == "c1_1000" else 5000
         Lq, Ld, d, k = 32, 300, 128, 100
         if name == "c1_rot":
@@ -151,6 +154,21 @@ def build(name: str, rotate: int, doc_align: int = 4) -> Workload:
                     "kernel": "stream_fwd_kernel + topk"}
             cpu = lambda: torch.topk(fm.maxsim_naive(Qc, Dc), k)  # noqa: E731
             sample = f"maxsim_naive fp32 + torch.topk over all {B} docs"
+        elif name == "c1_torch_topk":
+            cfg["workload"] = f"flash_maxsim + torch.topk k={k}: " + cfg["workload"]
+            cfg["k"] = k
+            steps = [lambda D=D: torch.topk(fm.flash_maxsim(Qd, D), k) for D in Ds]
+            roof = {"bound": "hbm", "amount": algo + B * 4 + k * 12, "unit": "GB/s",
+                    "kernel": "stream_fwd_kernel + torch.topk"}
+            cpu = lambda: torch.topk(fm.maxsim_naive(Qc, Dc), k)  # noqa: E731
+            sample = f"maxsim_naive fp32 + torch.topk over all {B} docs"
+        elif name == "c1_floor":
+            cfg["workload"] = "flash_maxsim + a one-element fill kernel: " + cfg["workload"]
+            one = torch.zeros(1, device=dev)
+            steps = [lambda D=D: (fm.flash_maxsim(Qd, D), one.zero_()) for D in Ds]
+            roof = {"bound": "hbm", "amount": algo, "unit": "GB/s", "kernel": "stream_fwd_kernel + fill"}
+            cpu = lambda: fm.maxsim_naive(Qc, Dc)  # noqa: E731
+            sample = f"maxsim_naive fp32 over all {B} docs"
         else:
             steps = [lambda D=D: fm.flash_maxsim(Qd, D) for D in Ds]
             roof = {"bound": "hbm", "amount": algo, "unit": "GB/s", "kernel": "stream_fwd_kernel"}

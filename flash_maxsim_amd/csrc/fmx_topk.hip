@@ -314,11 +314,13 @@ __device__ bool select_small_row(uint32_t (&raw)[E], int left, int k, float* vro
   const int nc = (int)*nsel_lds;
   if (flag[0] != 0 || nc > kTopkCountK || nc < want) return false;
 
-  constexpr int RB = 4;  // 16-byte reads per lane per batch
-  int G = 1;
-  while (2 * G <= 64 && 2 * G * nc <= NT) G *= 2;  // the groups of G lanes cover nc in one pass
-  const int span = 4 * RB * G;
-  const int padded = (nc + span - 1) / span * span;  // <= kTopkCountK: 4 * RB * G divides it
+  constexpr int RB = 8;                           // 16-byte reads per lane per batch
+  constexpr int GMAX = kTopkCountK / (4 * RB);    // one batch of GMAX lanes spans the buffer
+  // the largest power of two G <= GMAX with G * nc <= NT: the groups of G lanes cover nc in one pass
+  const int fit = NT / (nc > 0 ? nc : 1);
+  const int G = fit >= GMAX ? GMAX : fit <= 1 ? 1 : 1 << (31 - __builtin_clz(fit));
+  const int span = 4 * RB * G;                       // divides kTopkCountK
+  const int padded = (nc + span - 1) / span * span;  // <= kTopkCountK, as nc is
   const int part = tid & (G - 1);
   const f32x4_t* r4 = reinterpret_cast<const f32x4_t*>(rel);
   for (int j = tid / G; j < nc; j += NT / G) {  // all G lanes of a group share j
