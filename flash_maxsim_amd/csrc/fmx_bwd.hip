@@ -88,9 +88,16 @@ __device__ __forceinline__ int doc_len(const BwdArgs& a, int b) {
 
 // Stage 1 of dQ: one thread per (query token row r = qi*Lq + q, 8-wide k
 // chunk), one grid row per chunk of docs; ws[chunk][r][k] = sum over the
-// chunk's docs, in order.
-template <bool BF>
+// chunk's docs, in order. Docs go in batches of DB: the batch's argmax, upstream
+// gradients and lengths are loaded together, then its DB row chunks of D, so a
+// thread has DB gathers in flight instead of one (a doc at a time costs two
+// dependent memory round trips, and config 5's threads walk 32 docs each).
+// Positions past the chunk read its last doc again and, like empty docs, are
+// skipped (not multiplied by zero: a row may hold NaN padding); whether a doc
+// counts depends on the doc alone, so the skip is uniform over the wave.
+template <bool BF, bool FULL>
 __device__ __forceinline__ void dq_partial_block(const BwdArgs& a, int bx, int by) {
+  constexpr int DB = 8;
   const int nkc = (a.d + 7) >> 3;
   const int64_t rows = (int64_t)a.Nq * a.Lq;
   const int64_t tid = (int64_t)bx * 256 + threadIdx.x;
@@ -105,15 +112,44 @@ __device__ __forceinline__ void dq_partial_block(const BwdArgs& a, int bx, int b
   const uint16_t* D = static_cast<const uint16_t*>(a.D);
   const int32_t* am = a.argmax + (int64_t)qi * a.B * a.Lq + q;
   const float* g = a.grad + (int64_t)qi * a.g_n;
-#pragma unroll 4
-  for (int b = b0; b < b1; ++b) {
-    if (a.lengths && doc_len(a, b) == 0) continue;
-    const int j = clamp_index(am[(int64_t)b * a.Lq], a.Ld);
-    const float gb = g[(int64_t)b * a.g_b];
-    float x[8];
-    load8<BF>(D + (int64_t)b * a.sd_b + (int64_t)j * a.sd_l, k0, a.d, x);
+  for (int bb = b0; bb < b1; bb += DB) {
+    int j[DB];
+    float gb[DB];
+    int bi[DB];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = fmaf(gb, x[e], acc[e]);
+    for (int u = 0; u < DB; ++u) {
+      bi[u] = bb + u < b1 ? bb + u : b1 - 1;
+      j[u] = am[(int64_t)bi[u] * a.Lq];
+      gb[u] = g[(int64_t)bi[u] * a.g_b];
+    }
+    bool live[DB];
+#pragma unroll
+    for (int u = 0; u < DB; ++u) {
+      live[u] = bb + u < b1;
+      if (a.lengths) live[u] = live[u] && a.lengths[bi[u]] > 0;
+      j[u] = clamp_index(j[u], a.Ld);
+    }
+    float x[DB][8];
+#pragma unroll
+    for (int u = 0; u < DB; ++u) {
+      const uint16_t* row = D + (int64_t)bi[u] * a.sd_b + (int64_t)j[u] * a.sd_l;
+      if constexpr (FULL) {
+        const uint4 v = *reinterpret_cast<const uint4*>(row + k0);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x[u][2 * e] = Elem<BF>::to_f(w[e] & 0xffffu);
+          x[u][2 * e + 1] = Elem<BF>::to_f(w[e] >> 16);
+        }
+      } else {
+        load8<BF>(row, k0, a.d, x[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < DB; ++u)
+      if (live[u])
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = fmaf(gb[u], x[u][e], acc[e]);
   }
   float* out = a.ws + ((int64_t)by * rows + r) * a.d + k0;
 #pragma unroll
@@ -259,9 +295,9 @@ __device__ __forceinline__ void dd_write_block(const BwdArgs& a, int slab) {
   }
 }
 
-template <bool BF>
+template <bool BF, bool FULL>
 __global__ void __launch_bounds__(256) bwd_dq_partial_kernel(BwdArgs a) {
-  dq_partial_block<BF>(a, blockIdx.x, blockIdx.y);
+  dq_partial_block<BF, FULL>(a, blockIdx.x, blockIdx.y);
 }
 
 __global__ void __launch_bounds__(256) bwd_dd_index_kernel(BwdArgs a) {
@@ -281,8 +317,12 @@ hipError_t launch_bwd_t(const BwdArgs& a, hipStream_t s) {
   const int nkc = (a.d + 7) >> 3;
   if (a.dQ) {
     const int64_t threads = (int64_t)a.Nq * a.Lq * nkc;
-    hipLaunchKernelGGL(bwd_dq_partial_kernel<BF>, dim3((unsigned)((threads + 255) / 256), a.nchunk), dim3(256),
-                       0, s, a);
+    // FULL: every 8-wide chunk lies inside d, so each gather is one 16-byte load
+    const dim3 grid((unsigned)((threads + 255) / 256), a.nchunk);
+    if ((a.d & 7) == 0 && (a.sd_b & 7) == 0 && (a.sd_l & 7) == 0)
+      hipLaunchKernelGGL((bwd_dq_partial_kernel<BF, true>), grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((bwd_dq_partial_kernel<BF, false>), grid, dim3(256), 0, s, a);
     const int64_t n = (int64_t)a.Nq * a.Lq * a.d;
     hipLaunchKernelGGL(bwd_dq_finalize_kernel<BF>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
   }
@@ -297,12 +337,14 @@ hipError_t launch_bwd_t(const BwdArgs& a, hipStream_t s) {
 
 }  // namespace
 
-// Doc chunks of the dQ gather: enough (row, k-chunk, doc-chunk) threads to keep
-// the GPU's loads in flight (about 2^19), at most 64 chunks, at least 8 docs each.
+// Doc chunks of the dQ gather: about 2^17 (row, k-chunk, doc-chunk) threads,
+// at most 64 chunks, at least 8 docs each. Each thread keeps 8 gathers in
+// flight, so fewer, longer chunks keep the loads going with less partial-sum
+// traffic (config 5, 8 chunks: step 437 us; 16: 439; 32: 444).
 int bwd_dq_chunks(int B, int rows, int d) {
   if (B <= 0) return 1;
   const int64_t per_chunk = (int64_t)rows * ((d + 7) / 8);
-  int64_t n = ((int64_t)1 << 19) / (per_chunk > 0 ? per_chunk : 1);
+  int64_t n = ((int64_t)1 << 17) / (per_chunk > 0 ? per_chunk : 1);
   const int64_t by_docs = (B + 7) / 8;
   if (n > by_docs) n = by_docs;
   if (n > 64) n = 64;
