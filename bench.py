@@ -17,6 +17,8 @@ Configs (the driver's line is the default, c1):
              dependent launch after scoring
   c2         config 2, visual: Q[1024,128] x D[1000,1024,128]
   c3         config 3, batched: Q[100,32,128] x D[5000,300,128], shared docs
+  c3_zeros   config 3's shapes on all-zero Q and D: the same kernel and instruction
+             stream with no bits toggling, to show what the power limit costs
   c3_pq      batched with per-query docs (shared_docs=False):
              Q[100,32,128] x D[100,50,300,128]
   c4         config 4, uint8 docs [5000,1024,128], lengths U[32,1024]
@@ -202,16 +204,20 @@ def build(name: str, rotate: int, doc_align: int = 4) -> Workload:
         return Workload(cfg, steps, B, "docs/s", roof, cpu, n,
                         f"maxsim_naive fp32 over the first {n} docs in chunks of 50")
 
-    if name in ("c3", "c3_pq"):
+    if name in ("c3", "c3_pq", "c3_zeros"):
         Nq, Lq, Ld, d = 100, 32, 300, 128
-        B = 5000 if name == "c3" else 50
+        B = 50 if name == "c3_pq" else 5000
         Q = sim((Nq, Lq, d), 31, f16)
-        shape = (B, Ld, d) if name == "c3" else (Nq, B, Ld, d)
-        Dh = sim(shape, 32 if name == "c3" else 33, f16)
+        shape = (Nq, B, Ld, d) if name == "c3_pq" else (B, Ld, d)
+        Dh = sim(shape, 32 if name != "c3_pq" else 33, f16)
+        if name == "c3_zeros":
+            Q, Dh = torch.zeros_like(Q), torch.zeros_like(Dh)
         Qd = Q.to(dev)
         Ds = _copies(Dh.to(dev), rotate)
-        shared = name == "c3"
+        shared = name != "c3_pq"
         desc = "shared docs" if shared else "per-query docs (shared_docs=False)"
+        if name == "c3_zeros":
+            desc += ", all-zero inputs"
         cfg = {"workload": f"batched flash_maxsim Q[{Nq},{Lq},{d}] x D{list(shape)} fp16 {desc}", "Nq": Nq,
                "B": B, "Lq": Lq, "Ld": Ld, "d": d}
         if rotate > 1:
