@@ -223,7 +223,11 @@ hipError_t launch_q(const QuantArgs& a, hipStream_t s) {
   constexpr int RPB = 256 / LPR * R;
   const int64_t Ld4 = (a.Ld + 3) & ~(int64_t)3;
   const int64_t gx = (Ld4 + RPB - 1) / RPB;
-  const int64_t gy = a.B < 65535 ? a.B : 65535;
+  // two docs per workgroup (config 4's docs: 403 -> 394 us; four or more were slower).
+  // Rounding the product with the reciprocal and taking the correctly rounded
+  // quotient only near half-integers cut the arithmetic, but its registers
+  // halved the resident waves (394 -> 490 us).
+  const int64_t gy = (a.B + 1) / 2 < 65535 ? (a.B + 1) / 2 : 65535;
   if (gx > 0x7fffffff) return hipErrorInvalidValue;
   hipLaunchKernelGGL((quantize_kernel<SRC, LPR, CPL, R>), dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, s, a);
   return hipGetLastError();

@@ -51,6 +51,34 @@ def test_quantize_matches_oracle_bitwise(oracle_mod, dtype, d):
     np.testing.assert_array_equal(_bits(got[1]), _bits(t_s))
 
 
+def near_half_rows(seed, nrows, d):
+    """fp32 rows whose quotients (x - min) / scale fall on half-integers or
+    within 3 ulps of one: each row holds its min and max, then values at
+    min + (k + 0.5) * scale (scale as the formula computes it) nudged by -3..3
+    ulps, where rounding the product with the reciprocal could pick a different
+    code than rounding the correctly rounded quotient."""
+    rng = np.random.default_rng(seed)
+    out = np.empty((nrows, d), np.float32)
+    for r in range(nrows):
+        lo = np.float32(rng.standard_normal() * 0.1)
+        hi = np.float32(lo + np.float32(abs(rng.standard_normal()) + 0.05))
+        step = np.float32(np.float32(hi - lo) / np.float32(255.0))
+        k = rng.integers(0, 255, d - 2).astype(np.float32)
+        x = (lo + (k + np.float32(0.5)) * step).astype(np.float32)
+        x = (x.view(np.int32) + rng.integers(-3, 4, d - 2).astype(np.int32)).view(np.float32)
+        out[r, 0], out[r, 1], out[r, 2:] = lo, hi, np.clip(x, lo, hi)
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_quantize_quotients_near_half_integers(oracle_mod, dtype):
+    """Codes of values whose quotients sit on or next to half-integers equal the
+    oracle's (correctly rounded quotient, then round half to even) bit for bit."""
+    x = torch.from_numpy(near_half_rows(11, 16 * 128, 128)).reshape(16, 128, 128).to(dtype)
+    want = oracle_mod.quantize_int8(to_np32(x))[:3]
+    assert_quant_equal(fm.quantize_int8(x.to(DEV)), *want)
+
+
 def test_quantize_golden_fixture():
     f = np.load(ROOT / "tests" / "golden" / "quant.npz")
     got = fm.quantize_int8(torch.from_numpy(f["D"]).to(DEV))
