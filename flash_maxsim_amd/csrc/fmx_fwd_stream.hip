@@ -36,12 +36,13 @@ constexpr int kStreamWaves = 4;
 // the extra bytes in flight gain. fp16/bf16 tiles of 8 k-steps (d > 128) hold
 // 8 KB each: two in flight keep two or more waves per SIMD (four cost d = 192
 // and d = 256 with 64-token queries a quarter of their speed, at one wave).
-// uint8 passes of a full 128-VGPR query tile (128 rows at d <= 128) also keep
-// two tiles in flight, which with per-tile scale loads fits two waves per
-// SIMD in 256 VGPRs.
+// uint8 passes of a full 128-VGPR query tile (128 rows at d <= 128) keep four
+// tiles in flight in at most 242 VGPRs, two waves per SIMD (config 4's docs
+// under a 128-token query 117 -> 114 us, 5000 docs of 512 tokens 104 -> 102 us
+// against two tiles; three measured no better than two).
 template <int KIND, int NQB, int KS>
 constexpr int stream_depth() {
-  return (KIND != KIND_U8 && KS >= 8) || (KIND == KIND_U8 && NQB * KS >= 32) ? 2 : 4;
+  return (KIND != KIND_U8 && KS >= 8) ? 2 : 4;
 }
 
 // KMASK: d is not exactly 32*KS, so fragment slots past d must read as zero.
