@@ -291,15 +291,24 @@ stream_fwd_kernel(FwdArgs a) {
     T.m = u32x2_t{lane_fetch(gm, src), lane_fetch(gm, src + 1)};
   };
 
-  float m[NQB], m0[NQB];  // running max; m0 holds doc 0's once a wave reaches doc 1
+  float m[NQB];  // running max of the wave's current doc
   int mi[NQB];
-  int cur = 0;             // doc of the wave's running max
+  int cur = 0;   // doc of the wave's running max
 #pragma unroll
   for (int nb = 0; nb < NQB; ++nb) {
     m[nb] = -INFINITY;
-    m0[nb] = -INFINITY;
     mi[nb] = 0;
   }
+  // Doc dd's maxima of this wave, merged over the four row groups, into
+  // red_m[dd][wave] (scores only). Two-doc workgroups flush doc 0's when the
+  // wave reaches doc 1, so the tile loop carries one set of running maxima.
+  auto flush_max = [&](int dd) {
+#pragma unroll
+    for (int nb = 0; nb < NQB; ++nb) {
+      const float v = max_over_groups(m[nb]);
+      if (g == 0) red_m[dd][wave][nb * 16 + c] = v;
+    }
+  };
 
   // Tile i of the wave's sequence from ring slot T. The slot's refill (tile
   // i + P) is issued after the operands are taken and before the MFMAs:
@@ -313,11 +322,9 @@ stream_fwd_kernel(FwdArgs a) {
     const int tile = in1 ? sq - nt0 : sq;
     const int len = in1 ? len1 : len0;
     if (DOCS == 2 && in1 && cur == 0) {  // first tile of doc 1 for this wave
+      flush_max(0);
 #pragma unroll
-      for (int nb = 0; nb < NQB; ++nb) {
-        m0[nb] = m[nb];
-        m[nb] = -INFINITY;
-      }
+      for (int nb = 0; nb < NQB; ++nb) m[nb] = -INFINITY;
       cur = 1;
     }
     u32x4_t af[KS];
@@ -426,29 +433,26 @@ stream_fwd_kernel(FwdArgs a) {
   }
 
   // ---- merge the four row groups of each query token, then the four waves ----
-  if (DOCS == 2 && cur == 0) {  // the wave never reached doc 1
+  if constexpr (ARGMAX) {
 #pragma unroll
     for (int nb = 0; nb < NQB; ++nb) {
-      m0[nb] = m[nb];
-      m[nb] = -INFINITY;
-    }
-  }
-#pragma unroll
-  for (int dd = 0; dd < DOCS; ++dd) {
-#pragma unroll
-    for (int nb = 0; nb < NQB; ++nb) {
-      float v = (DOCS == 2 && dd == 0) ? m0[nb] : m[nb];
+      float v = m[nb];
       int ix = mi[nb];
-      if constexpr (ARGMAX) {
-        argmax_over_groups(v, ix);
-      } else {
-        v = max_over_groups(v);
-      }
+      argmax_over_groups(v, ix);
       if (g == 0) {
-        red_m[dd][wave][nb * 16 + c] = v;
-        if constexpr (ARGMAX) red_i[wave][nb * 16 + c] = ix;
+        red_m[0][wave][nb * 16 + c] = v;
+        red_i[wave][nb * 16 + c] = ix;
       }
     }
+  } else if constexpr (DOCS == 2) {
+    if (cur == 0) {  // the wave never reached doc 1
+      flush_max(0);
+#pragma unroll
+      for (int nb = 0; nb < NQB; ++nb) m[nb] = -INFINITY;
+    }
+    flush_max(1);
+  } else {
+    flush_max(0);
   }
   __syncthreads();
   const int dd = DOCS == 2 ? wave : 0;  // wave 0 sums doc 0, wave 1 doc 1
@@ -493,6 +497,150 @@ __global__ void __launch_bounds__(256) sum_passes_kernel(FwdArgs a, int npass) {
   a.scores[qi * a.ss_n + b * a.ss_b] = s;
 }
 
+
+// uint8 docs of one query with a full 128-row query tile (Lq in (64, 128],
+// d in (64, 128], vector path, padded docs), one doc per workgroup. The four
+// waves share each 16-token doc tile instead of each holding all 128 query
+// rows: wave w loads tokens 4w .. 4w+3 of the tile (lane (c, g): token
+// 4w + g, codes 8c .. 8c+7), dequantises them to fp16 as the reference does
+// (flash_maxsim_quant.py:89) and writes them to LDS; after one barrier every
+// wave reads the whole dequantised tile as MFMA A-fragments and multiplies it
+// by its own 32 query rows (two 16-row blocks). A wave then needs 80 VGPRs
+// instead of 242, so up to six share a SIMD instead of two and hide each
+// other's dequantisation, LDS and MFMA latency (config 4's docs under a
+// 128-token query 113.6 -> 104.4 us, 5000 docs of 512 tokens 103.1 -> 97.7
+// us, Q[96, 128] over 300-token docs 59.8 -> 53.1 us, one box).
+// Token rows past the doc's length load its last row again: a duplicate of a
+// valid row leaves the max unchanged, so no tile needs a mask.
+// Measured and not kept: two waves of 64 rows (LDS reads halved: within 1 %),
+// two tiles per barrier, the next tile's LDS reads issued before this tile's
+// MFMAs (+16 VGPRs: slower), several docs per workgroup as one tile sequence
+// (its cursor arithmetic cost more than the shared ring saved).
+constexpr int kShRow = 272;  // LDS bytes per dequantised token row; 256 + 16 spreads a b128 read's lanes over all banks
+
+template <int P>
+__global__ void __launch_bounds__(256) stream_u8_shared_kernel(FwdArgs a) {
+  static_assert(kStreamWaves == 4, "four waves of 32 query rows and 4 tile tokens each");
+  __shared__ __attribute__((aligned(16))) unsigned char tl[2][16 * kShRow];
+  __shared__ float part[kStreamWaves];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, g = lane >> 4;
+  const int b = blockIdx.x;
+  int len = a.lengths ? a.lengths[b] : a.Ld;
+  len = len < 0 ? 0 : (len > a.Ld ? a.Ld : len);
+  const int nt = (len + 15) >> 4;
+
+  // B-fragments of query rows 32 * wave + 16 * nb + c, k-step t: k = 32t + 8g .. +7
+  const rsrc_t rq = make_rsrc(a.Q, (uint32_t)(a.Lq_rows * a.sq_l * 2));
+  const int kp = a.d & ~7;
+  u32x4_t qf[2][4];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    const uint32_t rowoff = query_row_offset(a, b, 32 * wave + 16 * nb + c);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int k0 = 32 * t + 8 * g;
+      qf[nb][t] = ld16(rq, k0 < a.d ? rowoff + (uint32_t)(k0 * 2) : kOOB);
+      if (k0 == kp) qf[nb][t] &= prefix_mask16(a.d & 7);
+    }
+  }
+
+  const DocRes dr = make_doc_res<KIND_U8, true>(a, b, len);
+  const rsrc_t nul = make_rsrc(a.D, 0u);
+  // the lane's token row within a tile, the doc's last row, its byte in a row
+  // (codes at k >= d meet zero query values)
+  const int r0 = 4 * wave + g, rlast = len - 1;
+  const uint32_t kb = (uint32_t)(8 * c) < (uint32_t)a.d ? (uint32_t)(8 * c) : kOOB;
+  struct Slot {
+    u32x2_t v;
+    uint32_t s, m;
+  };
+  auto load = [&](Slot& S, int tile) {
+    int row = tile * 16 + r0;
+    row = row < rlast ? row : rlast;
+    const bool past = tile >= nt;  // the empty range: no access, a fixed load count
+    S.v = ld8(past ? nul : dr.d, (uint32_t)row * dr.rowb + kb);
+    S.s = ld2(past ? nul : dr.s, (uint32_t)row * 2u);
+    S.m = ld2(past ? nul : dr.m, (uint32_t)row * 2u);
+  };
+  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+  auto stage = [&](const Slot& S, int buf) {
+    // dequant_biased_f16 with the scale and min taken from the low halves by
+    // the packed ops' operand selects instead of widened first
+    const u32x4_t h = codes_to_f16_biased(S.v);
+    const _Float16 sc = __builtin_bit_cast(_Float16, (uint16_t)S.s), mn = __builtin_bit_cast(_Float16, (uint16_t)S.m);
+    const h2_t sc2 = {sc, sc}, mn2 = {mn, mn};
+    const h2_t bias = {(_Float16)kCodeBias, (_Float16)kCodeBias};
+    u32x4_t o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t hi = h[i];
+      const h2_t cd = __builtin_bit_cast(h2_t, hi) - bias;
+      o[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(cd, sc2, mn2));
+    }
+    *reinterpret_cast<u32x4_t*>(&tl[buf][r0 * kShRow + 16 * c]) = o;
+  };
+  float m[2] = {-INFINITY, -INFINITY};
+  auto score = [&](int buf) {
+    u32x4_t af[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      af[t] = *reinterpret_cast<const u32x4_t*>(&tl[buf][c * kShRow + (32 * t + 8 * g) * 2]);
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc = mfma16x16x32<false>(af[t], qf[nb][t], acc);
+      m[nb] = fold_max4(m[nb], acc[0], acc[1], acc[2], acc[3]);
+    }
+  };
+
+  // Tile i: loaded into ring slot i % P, staged into LDS buffer i & 1 (P is
+  // even), scored after the barrier. A buffer is rewritten two tiles later,
+  // after the next barrier, by which point every wave has read it.
+  static_assert(P % 2 == 0, "ring slots map to LDS buffers by parity");
+  Slot ring[P];
+#pragma unroll
+  for (int s = 0; s < P; ++s) load(ring[s], s);
+  int i0 = 0;
+  for (; i0 + P < nt; i0 += P) {
+#pragma unroll
+    for (int s = 0; s < P; ++s) {
+      stage(ring[s], s & 1);
+      load(ring[s], i0 + s + P);
+      __syncthreads();
+      score(s & 1);
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < P; ++s) {
+    if (i0 + s < nt) {  // uniform over the workgroup
+      stage(ring[s], s & 1);
+      __syncthreads();
+      score(s & 1);
+    }
+  }
+
+  // per wave: sum over its valid query rows of the max over the doc (-inf
+  // for an empty doc); then the four waves' sums in order
+  float sum = 0.f;
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    const float v = max_over_groups(m[nb]);
+    if (g == 0 && 32 * wave + 16 * nb + c < a.Lq) sum += v;
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) part[wave] = sum;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float total = part[0];
+#pragma unroll
+    for (int w = 1; w < kStreamWaves; ++w) total += part[w];
+    a.scores[(int64_t)b * a.ss_b] = total;
+  }
+}
+
 template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX, bool VEC = true, bool C16 = VEC>
 hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
   constexpr int QROWS = NQB * 16;
@@ -500,6 +648,13 @@ hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
   const int64_t items = (int64_t)a.Nq * a.B;
   if constexpr (KIND == KIND_U8 && !ARGMAX) {
     // uint8 docs of one query in one pass: two docs per workgroup.
+    // d in (64, 128] and 65-128 query tokens over padded docs: the shared-tile kernel.
+    if constexpr (NQB == 8 && KS == 4 && VEC) {
+      if (a.Nq == 1 && npass == 1 && !a.qidx && !a.tok_group) {
+        hipLaunchKernelGGL((stream_u8_shared_kernel<4>), dim3((unsigned)a.B), dim3(256), 0, s, a);
+        return hipGetLastError();
+      }
+    }
     if (a.Nq == 1 && npass == 1 && !a.qidx) {
       const dim3 grid((unsigned)((a.B + 1) / 2));
       // One scale range per pair when its offsets stay below 2^31 bytes: a

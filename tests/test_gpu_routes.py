@@ -246,3 +246,49 @@ def test_int8_padding_route_difference_bounded(oracle_mod):
     diff = np.abs(out128 - out129)
     print(f"uint8 padding 128 vs 129: max |diff| {diff.max():.3e}; fp16 rounding bound {rounding.min():.3e}")
     assert diff.max() < 1e-3
+
+
+@pytest.mark.parametrize("Lq, Ld, dst, d, B", [
+    (128, 1024, 128, 128, 9),   # 64 tiles per full doc, past the four-tile ring
+    (65, 300, 128, 128, 7),
+    (100, 132, 96, 96, 11),     # ring start and tail only
+    (97, 200, 112, 100, 6),     # d = 100 in rows of 112: a partial 8-wide chunk, codes past d in the row
+    (128, 516, 80, 80, 5),
+])
+def test_int8_shared_tile_route(oracle_mod, Lq, Ld, dst, d, B):
+    """Single uint8 queries of 65-128 tokens at d in (64, 128] over padded
+    docs with 16-byte code rows, aligned scale rows and Ld > 128: four waves
+    share each dequantised doc tile through LDS, and rows past a doc's length
+    load its last row again. Ragged lengths (0, 1, 15, 16, 17, a multiple of
+    the ring, Ld), a NaN scale in one doc's padding and a NaN min in another's
+    first token. Scores must match the oracle on the fp16-dequantised docs
+    within Higham's bound of the fp32 sums, the oracle's uint8 scores within
+    the fp16 bar, and a NaN only where a valid token carries one."""
+    from oracle.oracle_np import dequantize_fp16_np
+    from test_gpu_parity import MFMA_MARGIN, gamma
+
+    seed = 1800 + Lq + Ld + d
+    Q = sim((Lq, d), seed)
+    x = sim((B, Ld, dst), seed + 1, torch.float32)
+    codes_st, s, m = fm.quantize_int8(x)  # codes of all dst columns; the view uses the first d
+    codes = codes_st[..., :d]
+    lengths = torch.randint(1, Ld + 1, (B,), generator=torch.Generator().manual_seed(seed), dtype=torch.int32)
+    fixed = [Ld, 0, 1, 15, 16, 17, 64, Ld - 1, 33, 2, 31]
+    lengths[:min(B, len(fixed))] = torch.tensor(fixed[:B], dtype=torch.int32)
+    s[2, Ld - 1] = float("nan")  # doc 2 (1 token): past its length, never read
+    m[B - 1, 0] = float("nan")    # last doc: token 0 is valid
+    out = fm.flash_maxsim_int8(Q.to(DEV), codes.to(DEV), s.to(DEV), m.to(DEV), lengths.to(DEV))
+    got = out.double().cpu().numpy()
+    cn, ln, Qn = codes.contiguous().numpy(), lengths.numpy(), to_np32(Q)
+    ref32 = oracle_mod.maxsim_int8(Qn, cn, to_np32(s), to_np32(m), ln)
+    _check(out, ref32)
+    x16 = dequantize_fp16_np(cn, s.numpy(), m.numpy()).astype(np.float32)
+    ref16, _, best16 = oracle_mod.maxsim(Qn, x16, ln, want_argmax=True)
+    ref16 = ref16[0]
+    fin = np.isfinite(ref16)
+    assert np.array_equal(np.isfinite(got), fin) and np.isnan(got[B - 1]) and got[1] == -np.inf
+    valid = np.arange(Ld)[None, :, None] < ln[:, None, None]
+    A16 = np.nan_to_num(np.abs(x16.astype(np.float64))) @ np.abs(Qn.astype(np.float64)).T  # [B, Ld, Lq]
+    per = np.where(valid, MFMA_MARGIN * gamma(d) * A16, 0.0).max(axis=1).sum(axis=1)
+    bound = per + gamma(Lq) * np.where(np.isfinite(best16), np.abs(best16), 0.0).sum(axis=1)
+    assert (np.abs(got[fin] - ref16[fin]) <= bound[fin] * 1.001).all()
