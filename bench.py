@@ -292,7 +292,8 @@ def build(name: str, rotate: int, doc_align: int = 4) -> Workload:
             algo = tot * (d + 4) + Lq * d * 2 + B * 8
         if rotate > 1:
             cfg["rotated_doc_copies"] = len(steps)
-        roof = {"bound": "hbm", "amount": algo, "unit": "GB/s", "kernel": "stream_fwd_kernel"}
+        kern = "stream_u8_shared_kernel" if name == "c4_lq128" else "stream_fwd_kernel"
+        roof = {"bound": "hbm", "amount": algo, "unit": "GB/s", "kernel": kern}
         return Workload(cfg, steps, B, "docs/s", roof, cpu, n, sample)
 
     if name == "quant":
