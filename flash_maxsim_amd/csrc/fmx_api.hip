@@ -35,14 +35,16 @@ constexpr int64_t kOffLimit = (int64_t)1 << 31;  // buffer offsets stay below 2^
 
 // Kernel family and pass count for a forward shape.
 struct FwdPlan {
-  bool splitd;
+  bool wide;    // d > 4096: similarities through a workspace, then a reduction
+  bool splitd;  // 256 < d <= 4096
   int passes;
 };
 
 FwdPlan plan_fwd(int64_t Lq, int64_t d) {
   FwdPlan p;
-  p.splitd = d > 256;
-  p.passes = p.splitd ? fmx::splitd_fwd_passes((int)Lq, (int)d) : fmx::stream_fwd_passes((int)Lq, (int)d);
+  p.wide = d > fmx::kSplitMaxD;
+  p.splitd = !p.wide && d > 256;
+  p.passes = p.wide ? 1 : p.splitd ? fmx::splitd_fwd_passes((int)Lq, (int)d) : fmx::stream_fwd_passes((int)Lq, (int)d);
   return p;
 }
 
@@ -65,16 +67,17 @@ bool use_tiled(int64_t Nq, int64_t Lq, int64_t Ld, int64_t d, int shared_docs) {
 }
 
 // Streaming / split-d kernels: per-pass partial sums when the query needs
-// several passes.
-size_t stream_ws_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t d) {
+// several passes; wide kernels: a chunk of similarity rows.
+size_t stream_ws_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t Ld, int64_t d) {
   if (Lq < 1 || d < 1 || d > FMX_MAX_D || Nq < 1 || B < 1) return 0;
   const FwdPlan p = plan_fwd(Lq, d);
+  if (p.wide) return fmx::wide_fwd_workspace_bytes(Nq * B, Lq, Ld);
   return p.passes > 1 ? (size_t)p.passes * (size_t)Nq * (size_t)B * sizeof(float) : 0;
 }
 
 // Upper bound over the kernels fmx_fwd may pick for these sizes.
-size_t fwd_ws_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t d) {
-  size_t n = stream_ws_bytes(Nq, B, Lq, d);
+size_t fwd_ws_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t Ld, int64_t d) {
+  size_t n = stream_ws_bytes(Nq, B, Lq, Ld, d);
   if (Nq >= 1 && B >= 1 && Lq >= 1 && fmx::tiled_fwd_possible(Nq, Lq, (int)d)) {
     const fmx::TiledPlan p = fmx::tiled_fwd_plan(Nq, B, Lq, (int)d, device_cus());
     const size_t t = fmx::tiled_fwd_workspace_bytes(p, Nq, B);
@@ -152,13 +155,11 @@ const char* fmx_version(void) { return "0.1.0+mi355x"; }
 const char* fmx_last_error(void) { return g_err.c_str(); }
 
 size_t fmx_fwd_workspace_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t Ld, int64_t d) {
-  (void)Ld;
-  return fwd_ws_bytes(Nq, B, Lq, d);
+  return fwd_ws_bytes(Nq, B, Lq, Ld, d);
 }
 
 size_t fmx_fwd_int8_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld, int64_t d) {
-  (void)Ld;
-  return fwd_ws_bytes(1, B, Lq, d);  // the streaming, split-d and tiled kernels all take uint8 docs
+  return fwd_ws_bytes(1, B, Lq, Ld, d);  // every kernel family takes uint8 docs
 }
 
 }  // extern "C"
@@ -185,10 +186,13 @@ int fwd_impl(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, c
     tp = fmx::tiled_fwd_plan(Nq, B, Lq, (int)d, device_cus());
     need = fmx::tiled_fwd_workspace_bytes(tp, Nq, B);
   } else {
-    need = stream_ws_bytes(Nq, B, Lq, d);
+    need = stream_ws_bytes(Nq, B, Lq, Ld, d);
   }
+  const bool wide = plan_fwd(Lq, d).wide;
   if (noalloc) {
-    // the static scratch array stands in for the workspace
+    // the static scratch array stands in for the workspace; the wide kernels
+    // take as many items per chunk as it holds
+    if (wide && need > 0) need = fmx::wide_item_bytes(Lq, Ld);
     if (need > FMX_NOALLOC_SCRATCH_BYTES)
       return fail(FMX_ERR_UNSUPPORTED, "scratch of %zu bytes required, FMX_NOALLOC_SCRATCH_BYTES is %zu", need,
                   (size_t)FMX_NOALLOC_SCRATCH_BYTES);
@@ -230,6 +234,8 @@ int fwd_impl(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, c
   hipError_t e;
   if (tiled) {
     e = fmx::launch_tiled_fwd(kind, a, tp, argmax != nullptr, s);
+  } else if (wide) {
+    e = fmx::launch_wide_fwd(kind, a, argmax != nullptr, static_cast<float*>(workspace), workspace_bytes, s);
   } else if (plan_fwd(Lq, d).splitd) {
     e = fmx::launch_splitd_fwd(kind, a, argmax != nullptr, s);
   } else {
@@ -260,7 +266,7 @@ int int8_impl(const void* Q, int64_t q_stride_l, const uint8_t* D, int64_t d_str
     tp = fmx::tiled_fwd_plan(1, B, Lq, (int)d, device_cus());
     need = fmx::tiled_fwd_workspace_bytes(tp, 1, B);
   } else {
-    need = stream_ws_bytes(1, B, Lq, d);
+    need = stream_ws_bytes(1, B, Lq, Ld, d);
   }
   if (need > 0 && (!workspace || workspace_bytes < need))
     return fail(FMX_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
@@ -299,9 +305,12 @@ int int8_impl(const void* Q, int64_t q_stride_l, const uint8_t* D, int64_t d_str
   a.vec = (rows16 && sm8 && (tok_group || ((sm_stride_b & 3) == 0 && (Ld & 3) == 0))) ? 1 : 0;
   if (rows16 && aligned16(D)) a.vec |= 2;  // without bit 0: 16-byte code loads, per-tile scale loads
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const hipError_t e = tiled                   ? fmx::launch_tiled_fwd(fmx::KIND_U8, a, tp, false, s)
-                       : plan_fwd(Lq, d).splitd ? fmx::launch_splitd_fwd(fmx::KIND_U8, a, false, s)
-                                                : fmx::launch_stream_fwd(fmx::KIND_U8, a, false, s);
+  const FwdPlan p = plan_fwd(Lq, d);
+  const hipError_t e = tiled    ? fmx::launch_tiled_fwd(fmx::KIND_U8, a, tp, false, s)
+                       : p.wide ? fmx::launch_wide_fwd(fmx::KIND_U8, a, false, static_cast<float*>(workspace),
+                                                       workspace_bytes, s)
+                       : p.splitd ? fmx::launch_splitd_fwd(fmx::KIND_U8, a, false, s)
+                                  : fmx::launch_stream_fwd(fmx::KIND_U8, a, false, s);
   return hip_status(e, "fmx_fwd_int8 launch");
 }
 
@@ -345,17 +354,18 @@ int fmx_fwd_noalloc(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stri
 namespace {
 
 // fmx_fwd_topk's workspace: fmx_fwd's, then fmx_topk's (256-byte aligned).
-size_t topk_fwd_part(int64_t B, int64_t Lq, int64_t d) { return (fwd_ws_bytes(1, B, Lq, d) + 255) & ~(size_t)255; }
+size_t topk_fwd_part(int64_t B, int64_t Lq, int64_t Ld, int64_t d) {
+  return (fwd_ws_bytes(1, B, Lq, Ld, d) + 255) & ~(size_t)255;
+}
 
 }  // namespace
 
 extern "C" {
 
 size_t fmx_fwd_topk_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld, int64_t d, int64_t k) {
-  (void)Ld;
   // the scoring part is needed for any k (k = 0 still scores the docs)
   if (B < 1 || Lq < 1 || d < 1 || d > FMX_MAX_D || k < 0) return 0;
-  return topk_fwd_part(B, Lq, d) + fmx_topk_workspace_bytes(1, B, k);
+  return topk_fwd_part(B, Lq, Ld, d) + fmx_topk_workspace_bytes(1, B, k);
 }
 
 int fmx_fwd_topk(int dtype, const void* Q, int64_t q_stride_l, const void* D, int64_t d_stride_b,
@@ -373,7 +383,7 @@ int fmx_fwd_topk(int dtype, const void* Q, int64_t q_stride_l, const void* D, in
     return fail(FMX_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
   if (reinterpret_cast<uintptr_t>(workspace) & 255u) return fail(FMX_ERR_INVALID, "workspace must be 256-byte aligned");
   char* w = static_cast<char*>(workspace);
-  const size_t fws = B > 0 ? topk_fwd_part(B, Lq, d) : 0;
+  const size_t fws = B > 0 ? topk_fwd_part(B, Lq, Ld, d) : 0;
   rc = fmx_fwd(dtype, Q, 0, q_stride_l, D, d_stride_b, d_stride_l, lengths, scores, 0, 1, nullptr, 1, B, Lq, Ld, d, 1,
                fws ? w : nullptr, fws, stream);
   if (rc || B == 0 || k == 0) return rc;
@@ -382,7 +392,7 @@ int fmx_fwd_topk(int dtype, const void* Q, int64_t q_stride_l, const void* D, in
 }
 
 size_t fmx_fwd_packed_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld_max, int64_t d) {
-  return fwd_ws_bytes(1, B, Lq, d);
+  return fwd_ws_bytes(1, B, Lq, Ld_max, d);
 }
 
 int fmx_fwd_packed(int dtype, const void* Q, int64_t q_stride_l, int64_t Lq, const void* D, int64_t d_stride_l,
@@ -397,7 +407,7 @@ int fmx_fwd_packed(int dtype, const void* Q, int64_t q_stride_l, int64_t Lq, con
 }
 
 size_t fmx_fwd_int8_packed_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld_max, int64_t d) {
-  return fwd_ws_bytes(1, B, Lq, d);
+  return fwd_ws_bytes(1, B, Lq, Ld_max, d);
 }
 
 int fmx_fwd_int8_packed(const void* Q, int64_t q_stride_l, int64_t Lq, const uint8_t* codes, int64_t c_stride_l,
@@ -492,8 +502,7 @@ int fmx_topk(const float* scores, int64_t s_stride_n, int64_t Nq, int64_t B, int
 }
 
 size_t fmx_fwd_sparse_workspace_bytes(int64_t B, int64_t K, int64_t Ld, int64_t d) {
-  (void)Ld;
-  return stream_ws_bytes(1, B, K, d);
+  return stream_ws_bytes(1, B, K, Ld, d);
 }
 
 int fmx_fwd_sparse(int dtype, const void* Q, int64_t q_stride_l, int64_t Lq, const void* D,
@@ -508,7 +517,7 @@ int fmx_fwd_sparse(int dtype, const void* Q, int64_t q_stride_l, int64_t Lq, con
   if (B == 0) return ok();
   if (!Q || !D || !scores || !indices) return fail(FMX_ERR_INVALID, "Q, D, indices and scores must be non-null");
   if (!aligned16(Q) || !aligned16(D)) return fail(FMX_ERR_INVALID, "Q and D must be 16-byte aligned");
-  const size_t need = stream_ws_bytes(1, B, K, d);
+  const size_t need = stream_ws_bytes(1, B, K, Ld, d);
   if (need > 0 && (!workspace || workspace_bytes < need))
     return fail(FMX_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
 
@@ -537,8 +546,10 @@ int fmx_fwd_sparse(int dtype, const void* Q, int64_t q_stride_l, int64_t Lq, con
   a.shared_docs = 1;
   const int kind = dtype == FMX_DTYPE_BF16 ? fmx::KIND_BF16 : fmx::KIND_F16;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const hipError_t e = plan_fwd(K, d).splitd ? fmx::launch_splitd_fwd(kind, a, false, s)
-                                             : fmx::launch_stream_fwd(kind, a, false, s);
+  const FwdPlan p = plan_fwd(K, d);
+  const hipError_t e = p.wide     ? fmx::launch_wide_fwd(kind, a, false, static_cast<float*>(workspace), workspace_bytes, s)
+                       : p.splitd ? fmx::launch_splitd_fwd(kind, a, false, s)
+                                  : fmx::launch_stream_fwd(kind, a, false, s);
   return hip_status(e, "fmx_fwd_sparse launch");
 }
 

@@ -72,6 +72,16 @@ int splitd_fwd_nqb(int Lq, int d);    // 16-token query blocks per pass
 int splitd_fwd_passes(int Lq, int d); // > 1: partial sums in FwdArgs::partial
 hipError_t launch_splitd_fwd(int kind, const FwdArgs& a, bool with_argmax, hipStream_t s);
 
+// Wide kernels, d > 4096: the similarities of a chunk of (query, doc) items go
+// to a workspace S [items, Lq, Ld rounded up to 16] (fp32), then a reduction
+// takes each query token's max (and argmax) and the sum. The workspace holds
+// ws_bytes / wide_item_bytes(Lq, Ld) items per chunk (at least one).
+constexpr int kSplitMaxD = 4096;
+constexpr size_t kWideChunkBytes = (size_t)64 << 20;  // preferred S chunk
+size_t wide_item_bytes(int64_t Lq, int64_t Ld);
+size_t wide_fwd_workspace_bytes(int64_t items, int64_t Lq, int64_t Ld);
+hipError_t launch_wide_fwd(int kind, const FwdArgs& a, bool with_argmax, float* ws, size_t ws_bytes, hipStream_t s);
+
 // Tiled kernel (MFMA-bound regime): persistent 8- or 4-wave workgroups keep a
 // block of query rows in VGPRs and stream shared docs through LDS. d <= 256.
 // fp16/bf16 docs, and uint8 docs (dequantised to fp16 on their way to LDS;

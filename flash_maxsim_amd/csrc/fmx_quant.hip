@@ -233,6 +233,74 @@ hipError_t launch_q(const QuantArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Rows wider than 4096 elements: one workgroup per token row, each thread
+// taking elements tid, tid + 256, ...: the min and max meet across the
+// workgroup, then a second pass over the row (from cache) writes the codes.
+// Same arithmetic, element for element, as quantize_kernel.
+template <int SRC>
+__global__ void __launch_bounds__(256) quantize_wide_kernel(QuantArgs a) {
+  __shared__ float wlo[4], whi[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool packed = a.tok_group != nullptr;
+  const int64_t j = blockIdx.x;
+  for (int64_t b = blockIdx.y; b < a.B; b += gridDim.y) {
+    int64_t len = a.Ld;
+    if (a.lengths && packed) {
+      len = a.lengths[b];
+      len = len < 0 ? 0 : (len > a.Ld ? a.Ld : len);
+    }
+    const int64_t jend = packed ? ((len + 3) & ~(int64_t)3) : a.Ld;
+    if (j >= jend) continue;
+    const int64_t obase = packed ? 4 * a.tok_group[b] : b * a.Ld;
+    const int64_t orow = obase + j;
+    if (packed && (orow < 0 || orow >= a.tok_rows)) continue;
+    uint8_t* crow = a.codes + orow * a.c_stride_l;
+    const int64_t smi = packed ? orow : b * a.sm_stride_b + j;
+    uint16_t* sp = static_cast<uint16_t*>(a.scales) + smi;
+    uint16_t* mp = static_cast<uint16_t*>(a.mins) + smi;
+    if (j >= len) {  // packed: zero rows up to the next multiple of 4
+      for (int64_t k = tid; k < a.d; k += 256) crow[k] = 0;
+      if (tid == 0) {
+        *sp = 0;
+        *mp = 0;
+      }
+      continue;
+    }
+    const char* src = static_cast<const char*>(a.src) + (b * a.s_stride_b + j * a.s_stride_l) * a.esz;
+    float lo = INFINITY, hi = -INFINITY;
+    for (int64_t k = tid; k < a.d; k += 256) {
+      const float x = src_elem<SRC>(src, k);
+      lo = mm<false>(lo, x);
+      hi = mm<true>(hi, x);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      lo = mm<false>(lo, __shfl_xor(lo, off));
+      hi = mm<true>(hi, __shfl_xor(hi, off));
+    }
+    if (lane == 0) {
+      wlo[wave] = lo;
+      whi[wave] = hi;
+    }
+    __syncthreads();
+    lo = mm<false>(mm<false>(wlo[0], wlo[1]), mm<false>(wlo[2], wlo[3]));
+    hi = mm<true>(mm<true>(whi[0], whi[1]), mm<true>(whi[2], whi[3]));
+    __syncthreads();  // wlo / whi are rewritten for the next doc
+    float step = (hi - lo) / 255.0f;
+    if (step < 1e-8f) step = 1e-8f;
+    const float rstep = 1.0f / step;
+    for (int64_t k = tid; k < a.d; k += 256) {
+      float v = __builtin_rintf(div_rn<SRC == 0>(src_elem<SRC>(src, k) - lo, step, rstep));
+      v = fminf(fmaxf(v, 0.f), 255.f);
+      crow[k] = (uint8_t)v;
+    }
+    if (tid == 0) {
+      *sp = __builtin_bit_cast(uint16_t, (_Float16)step);
+      *mp = __builtin_bit_cast(uint16_t, (_Float16)lo);
+    }
+  }
+}
+
 template <int SRC>
 hipError_t dispatch_q(const QuantArgs& a, hipStream_t s) {
   const int chunks = (int)((a.d + 7) / 8);
@@ -245,7 +313,12 @@ hipError_t dispatch_q(const QuantArgs& a, hipStream_t s) {
   if (chunks <= 64) return launch_q<SRC, 64, 1>(a, s);
   if (chunks <= 128) return launch_q<SRC, 64, 2>(a, s);
   if (chunks <= 256) return launch_q<SRC, 64, 4>(a, s);
-  return launch_q<SRC, 64, 8>(a, s);  // d <= 4096
+  if (chunks <= 512) return launch_q<SRC, 64, 8>(a, s);  // d <= 4096
+  const int64_t Ld4 = (a.Ld + 3) & ~(int64_t)3;
+  const int64_t gy = a.B < 65535 ? a.B : 65535;
+  if (Ld4 > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(quantize_wide_kernel<SRC>, dim3((unsigned)Ld4, (unsigned)gy), dim3(256), 0, s, a);
+  return hipGetLastError();
 }
 
 }  // namespace

@@ -41,7 +41,11 @@ extern "C" {
 #define FMX_DTYPE_BF16 1
 #define FMX_DTYPE_F32 2 /* fmx_quantize_int8 sources only */
 
-#define FMX_MAX_D 4096
+/* Widest d. Up to 4096 the forward kernels hold each query slice in
+ * registers; wider rows (which the reference reaches by padding d to a power
+ * of two, flash_maxsim/flash_maxsim.py:8-9) compute similarities into the
+ * workspace in chunks of docs and reduce them in a second kernel. */
+#define FMX_MAX_D 65536
 #define FMX_MAX_TOPK 8192
 #define FMX_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20) /* per GPU, see fmx_fwd_noalloc */
 
@@ -81,8 +85,10 @@ size_t fmx_fwd_workspace_bytes(int64_t Nq, int64_t B, int64_t Lq, int64_t Ld, in
  * tight serving loops, harnesses that forbid hipMalloc. No counterpart in the
  * reference. Same arguments, results and errors as fmx_fwd without the
  * workspace: the partial sums fmx_fwd keeps in its workspace (queries that
- * take several passes, queries straddling row blocks) go to a static device
- * array of FMX_NOALLOC_SCRATCH_BYTES on each GPU, held until the process
+ * take several passes, queries straddling row blocks) and, for d > 4096, its
+ * chunks of similarities (as many (query, doc) items per chunk as fit, each
+ * Lq x (Ld rounded up to 16) x 4 bytes) go to a static device array of
+ * FMX_NOALLOC_SCRATCH_BYTES on each GPU, held until the process
  * ends. A call whose chosen kernels need more scratch than that fails with
  * FMX_ERR_UNSUPPORTED before any launch; fmx_fwd_workspace_bytes bounds that
  * need over every kernel route the sizes allow, so a call can succeed where

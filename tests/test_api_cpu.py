@@ -70,7 +70,8 @@ def _fwd(lib, **kw):
 
 @pytest.mark.parametrize("kw, code, text", [
     (dict(dtype=7), FMX_ERR_INVALID, "dtype"),
-    (dict(d=4104, ql=4104, dl=4104, db=4104 * 300), FMX_ERR_UNSUPPORTED, "FMX_MAX_D"),
+    (dict(d=65544, ql=65544, dl=65544, db=65544 * 300), FMX_ERR_UNSUPPORTED, "FMX_MAX_D"),
+    (dict(d=8192, ql=8192, dl=8192, db=8192 * 300), FMX_ERR_WORKSPACE, "workspace"),  # d > 4096: similarity chunks
     (dict(ql=100), FMX_ERR_INVALID, "Q row stride"),
     (dict(dl=120), FMX_ERR_INVALID, "D row stride"),
     (dict(db=300 * 128 + 4), FMX_ERR_INVALID, "doc stride"),

@@ -2,7 +2,8 @@
 
 Each case needs scratch (fmx_fwd_workspace_bytes > 0): a query of several
 passes over per-query docs (streaming kernel), a query of several passes at
-d = 1024 (split-d kernel), and queries straddling row blocks (tiled kernel).
+d = 1024 (split-d kernel), queries straddling row blocks (tiled kernel), and
+d > 4096 (similarity chunks, fewer items per chunk in the scratch).
 Two calls in a row, the second smaller, must each give scores bit-identical
 to fmx_fwd's on the same inputs: both run the same kernels in the same order,
 one with a caller workspace and one with the library's static scratch.
@@ -25,6 +26,9 @@ CASES = {
     "stream_passes": [(3, 300, 40, 90, 128, 0), (2, 200, 17, 50, 128, 0)],
     "splitd_passes": [(1, 300, 20, 70, 1024, 1), (1, 150, 9, 33, 1024, 1)],
     "tiled_straddle": [(3, 700, 30, 90, 128, 1), (2, 650, 11, 40, 128, 1)],
+    # d > 4096: similarity chunks; fmx_fwd's workspace holds all 70 items, the
+    # scratch 64 per chunk (256 KB each), so the noalloc call runs two chunks
+    "wide_chunks": [(1, 128, 70, 512, 4104, 1), (1, 64, 20, 100, 5000, 1)],
 }
 
 
