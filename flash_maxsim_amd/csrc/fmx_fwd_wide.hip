@@ -6,9 +6,9 @@
 //  * wide_sim_kernel: each wave computes the similarities of 32 doc tokens
 //    (two 16-token tiles) against up to 128 query tokens (eight 16-token
 //    blocks) over the whole of d on v_mfma_f32_16x16x32 with fp32
-//    accumulation, reading doc fragments once from HBM and query fragments
-//    from L2 at every 32-wide k-step, and stores them to the workspace
-//    S[item][query token][doc token];
+//    accumulation, reading doc fragments once from HBM and the workgroup's
+//    query rows through LDS four 32-wide k-steps at a time, and stores them
+//    to the workspace S[item][query token][doc token];
 //  * wide_reduce_kernel: per item, the max over each query token's row of S
 //    up to the doc's length (the first index reaching it, with torch.max's NaN
 //    rule, when the argmax is requested), summed over query tokens in order.
@@ -19,14 +19,18 @@
 // Bound: HBM for the doc stream at small query counts; the S round trip adds
 // 8 x Lq bytes per doc token to the d x 2 (fp16) read (1.6 % at Lq = 32,
 // d = 8192).
+#include <type_traits>
+
 #include "fmx_kernels.h"
 #include "fmx_tile.h"
 
 namespace fmx {
 namespace {
 
-constexpr int kWideQB = 8;  // 16-token query blocks per similarity pass
-constexpr int kWideTW = 2;  // 16-token doc tiles per wave
+constexpr int kWideQB = 8;     // 16-token query blocks per similarity pass
+constexpr int kWideTW = 2;     // 16-token doc tiles per wave
+constexpr int kWideKC = 4;     // k-steps per staged query chunk
+constexpr int kWideQRow = 80;  // LDS bytes per query row and k-step: 64 + 16 spreads a b128 read over all banks
 
 // Item (query qi, doc b) of the call, its doc row and the doc's length.
 __device__ __forceinline__ void wide_item(const FwdArgs& a, int item, int& qi, int& b, int64_t& drow, int& len) {
@@ -39,26 +43,58 @@ __device__ __forceinline__ void wide_item(const FwdArgs& a, int item, int& qi, i
 
 // blockIdx.x: item of the chunk; blockIdx.y: group of 4 * kWideTW doc tiles;
 // blockIdx.z: group of kWideQB query blocks. S rows are ldp floats apart.
+// The workgroup's 128 query rows come through LDS kWideKC k-steps at a time
+// (each thread loads 16 bytes of two rows per k-step), so L2 serves each
+// query fragment once per workgroup instead of once per wave; the next
+// chunk's query and doc fragments are loaded while this chunk's MFMAs run.
 template <int KIND>
 __global__ void __launch_bounds__(256) wide_sim_kernel(FwdArgs a, float* S, int item0, int ldp) {
   constexpr bool U8 = KIND == KIND_U8;
   constexpr int ESZ = KindInfo<KIND>::esz;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  __shared__ __attribute__((aligned(16))) unsigned char qs[kWideKC][16 * kWideQB * kWideQRow];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 15, g = lane >> 4;
   const int il = blockIdx.x, item = item0 + il;
   int qi, b, len;
   int64_t drow;
   wide_item(a, item, qi, b, drow, len);
+  if (blockIdx.y * 4 * kWideTW * 16 >= len) return;  // the whole workgroup: before any barrier
   const int tile0 = (blockIdx.y * 4 + wave) * kWideTW;
-  if (tile0 * 16 >= len) return;  // waves are independent here: no barrier follows
+  const bool active = tile0 * 16 < len;  // wave-uniform; inactive waves still stage query rows
   const int qb0 = blockIdx.z * kWideQB;
   const int nqb = (a.Lq + 15) / 16 - qb0 < kWideQB ? (a.Lq + 15) / 16 - qb0 : kWideQB;
+  const int kp = a.d & ~7;
+  const u32x4_t pmask = prefix_mask16(a.d & 7);
 
+  // query staging: thread (r, p) = (tid / 4, tid % 4) loads bytes 16p .. 16p+15 of
+  // each k-step of rows r and r + 64 of the block group
   const rsrc_t rq = make_rsrc((const char*)a.Q + (int64_t)qi * a.sq_n * 2, (uint32_t)(a.Lq_rows * a.sq_l * 2));
-  uint32_t qrow[kWideQB];
+  const int sr = tid >> 2, sp = tid & 3;
+  uint32_t qoff[2];
 #pragma unroll
-  for (int nb = 0; nb < kWideQB; ++nb) qrow[nb] = nb < nqb ? query_row_offset(a, b, (qb0 + nb) * 16 + c) : kOOB;
+  for (int h = 0; h < 2; ++h) {
+    const int r = sr + 64 * h;
+    qoff[h] = r < 16 * nqb ? query_row_offset(a, b, qb0 * 16 + r) : kOOB;
+  }
+  u32x4_t vq[2][kWideKC];
+  auto qload = [&](int kc) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int t = 0; t < kWideKC; ++t) {
+        const int k = (kc * kWideKC + t) * 32 + 8 * sp;
+        vq[h][t] = ld16(rq, k < a.d ? qoff[h] + (uint32_t)(k * 2) : kOOB);
+        if (k == kp) vq[h][t] &= pmask;
+      }
+  };
+  auto qstore = [&]() {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int t = 0; t < kWideKC; ++t)
+        *reinterpret_cast<u32x4_t*>(&qs[t][(sr + 64 * h) * kWideQRow + 16 * sp]) = vq[h][t];
+  };
 
   // doc rows: each lane loads token tile*16 + c, as in load_tile; rows past
   // the length read zeros and their similarities are never reduced
@@ -74,8 +110,23 @@ __global__ void __launch_bounds__(256) wide_sim_kernel(FwdArgs a, float* S, int 
       mn[w] = ld2(dr.m, dr.sm + (uint32_t)row * 2u);
     }
   }
-  const int kp = a.d & ~7;
-  const u32x4_t pmask = prefix_mask16(a.d & 7);
+  using Raw = typename std::conditional<U8, u32x2_t, u32x4_t>::type;
+  Raw vd[kWideTW][kWideKC];
+  auto dload = [&](int kc) {
+#pragma unroll
+    for (int w = 0; w < kWideTW; ++w)
+#pragma unroll
+      for (int t = 0; t < kWideKC; ++t) {
+        const int k0 = (kc * kWideKC + t) * 32 + 8 * g;
+        const uint32_t o = k0 < a.d ? drowoff[w] + (uint32_t)(k0 * ESZ) : kOOB;
+        if constexpr (U8) {
+          vd[w][t] = ld8(dr.d, active ? o : kOOB);
+        } else {
+          vd[w][t] = ld16(dr.d, active ? o : kOOB);
+          if (k0 == kp) vd[w][t] &= pmask;  // the row's elements past d are not the doc's
+        }
+      }
+  };
 
   f32x4_t acc[kWideTW][kWideQB];
 #pragma unroll
@@ -83,31 +134,43 @@ __global__ void __launch_bounds__(256) wide_sim_kernel(FwdArgs a, float* S, int 
 #pragma unroll
     for (int nb = 0; nb < kWideQB; ++nb) acc[w][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int ksteps = (a.d + 31) / 32;
-  for (int t = 0; t < ksteps; ++t) {
-    const int k0 = 32 * t + 8 * g;
-    const bool in = k0 < a.d;
-    u32x4_t af[kWideTW];
+  const int nkc = (a.d + 32 * kWideKC - 1) / (32 * kWideKC);
+  qload(0);
+  dload(0);
+  for (int kc = 0; kc < nkc; ++kc) {
+    __syncthreads();  // the previous chunk's readers are done with qs
+    qstore();
+    u32x4_t af[kWideTW][kWideKC];
 #pragma unroll
-    for (int w = 0; w < kWideTW; ++w) {
-      if constexpr (U8) {
-        const u32x2_t raw = ld8(dr.d, in ? drowoff[w] + (uint32_t)k0 : kOOB);
-        af[w] = dequant_biased_f16(codes_to_f16_biased(raw), sc[w], mn[w]);
-      } else {
-        af[w] = ld16(dr.d, in ? drowoff[w] + (uint32_t)(k0 * ESZ) : kOOB);
-        if (k0 == kp) af[w] &= pmask;  // the row's elements past d are not the doc's
+    for (int w = 0; w < kWideTW; ++w)
+#pragma unroll
+      for (int t = 0; t < kWideKC; ++t) {
+        if constexpr (U8) {
+          af[w][t] = dequant_biased_f16(codes_to_f16_biased(vd[w][t]), sc[w], mn[w]);
+        } else {
+          af[w][t] = vd[w][t];
+        }
       }
+    __syncthreads();
+    if (kc + 1 < nkc) {
+      qload(kc + 1);
+      dload(kc + 1);
     }
+    if (active) {
 #pragma unroll
-    for (int nb = 0; nb < kWideQB; ++nb) {
-      if (nb < nqb) {  // uniform
-        u32x4_t bq = ld16(rq, in ? qrow[nb] + (uint32_t)(k0 * 2) : kOOB);
-        if (k0 == kp) bq &= pmask;
+      for (int t = 0; t < kWideKC; ++t)
 #pragma unroll
-        for (int w = 0; w < kWideTW; ++w) acc[w][nb] = mfma16x16x32<KindInfo<KIND>::bf>(af[w], bq, acc[w][nb]);
-      }
+        for (int nb = 0; nb < kWideQB; ++nb) {
+          if (nb < nqb) {  // uniform
+            const u32x4_t bq = *reinterpret_cast<const u32x4_t*>(&qs[t][(16 * nb + c) * kWideQRow + 16 * g]);
+#pragma unroll
+            for (int w = 0; w < kWideTW; ++w)
+              acc[w][nb] = mfma16x16x32<KindInfo<KIND>::bf>(af[w][t], bq, acc[w][nb]);
+          }
+        }
     }
   }
+  if (!active) return;
 
   // result lane (c, g): doc tokens tile*16 + 4g .. +3 of query token 16*qb + c
   float* Si = S + (int64_t)il * a.Lq * ldp;
