@@ -24,6 +24,9 @@
 // rounding.
 // Queries longer than 16*NQB tokens run as blockIdx.y passes whose partial sums
 // a second kernel adds in pass order.
+// Single uint8 queries of 65-128 tokens over padded docs at d in (64, 128] run
+// stream_u8_shared_kernel instead: its four waves share each doc tile through
+// LDS and hold 32 query rows each (see there).
 #include "fmx_kernels.h"
 #include "fmx_tile.h"
 
