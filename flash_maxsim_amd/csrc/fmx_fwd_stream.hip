@@ -48,6 +48,25 @@ constexpr int stream_depth() {
   return (KIND != KIND_U8 && KS >= 8) ? 2 : 4;
 }
 
+// Doc tiles through a per-wave LDS ring (stream_fwd_kernel's DMA path):
+// fp16/bf16 rows of exactly 128 elements scored without argmax, outside the
+// two-tile ring of short doc pairs (PD = 2). Two tiles in flight per wave
+// (8 KB of LDS each way), so a CU holds three workgroups.
+template <int KIND, int KS, bool KMASK, bool ARGMAX, int PD>
+constexpr bool stream_dma() {
+  return KIND != KIND_U8 && KS == 4 && !KMASK && !ARGMAX && PD == 0;
+}
+constexpr int kStreamDmaDepth = 2;
+constexpr int kTileBytes = 16 * 256;  // a DMA tile: 16 rows of 128 fp16/bf16 elements
+
+// Waits until at most N vector-memory instructions of this wave are in
+// flight (vmcnt(N); the other counters at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+  __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
+}
+
 // KMASK: d is not exactly 32*KS, so fragment slots past d must read as zero.
 // VEC: uint8 vector load path (FwdArgs::vec); true for fp16/bf16.
 // DOCS = 2 (one pass, no argmax; uint8 docs of one query, and fp16/bf16 docs
@@ -77,7 +96,20 @@ template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX, bool VEC, int DOCS
           bool C16 = VEC>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(stream_min_waves<KIND, NQB, KS, VEC, DOCS>())))
 stream_fwd_kernel(FwdArgs a) {
-  constexpr int NW = kStreamWaves, P = PD ? PD : stream_depth<KIND, NQB, KS>(), QROWS = NQB * 16;
+  // DMA: each wave's ring lives in LDS. A tile's 16 rows of 256 bytes come by
+  // LDS DMA loads of whole 128-byte lines (four rows per instruction, 16-byte
+  // chunks swizzled by row, chunk j of row r at j ^ r, so the fragment reads
+  // spread over all banks) with the nt cache policy, and the MFMA fragments
+  // are read from LDS. With whole lines per load instruction the nt policy
+  // streams them: config 1 60.8 -> 55.2 us, per-query docs 61.7 -> 56.0 us,
+  // Q[128,128] over 1000 docs of 1024 tokens 46.8 -> 44.1 us (a plain read of
+  // config 1's docs: 60.1 -> 55.5 us with nt). The VGPR ring's loads follow
+  // the MFMA fragment order, which touches each line with two instructions;
+  // nt made those 17 % slower. Short doc pairs (the PD = 2 ring) keep VGPR
+  // tiles: 5000 docs of 77 tokens 18.3 -> 19.9 us through LDS.
+  constexpr bool DMA = stream_dma<KIND, KS, KMASK, ARGMAX, PD>();
+  constexpr int NW = kStreamWaves, P = PD ? PD : (DMA ? kStreamDmaDepth : stream_depth<KIND, NQB, KS>()),
+                QROWS = NQB * 16;
   constexpr int ESZ = KindInfo<KIND>::esz;
   constexpr bool BF = KindInfo<KIND>::bf;
   constexpr bool U8 = KIND == KIND_U8;
@@ -218,7 +250,9 @@ stream_fwd_kernel(FwdArgs a) {
   static_assert(!GSM || P == 4 || P == 2, "group scale loads map 16 lanes per tile slot");
   static_assert(!JOINT || DOCS == 2, "a joint scale range serves two-doc group loads");
   const rsrc_t nul = make_rsrc(a.D, 0u);
-  auto seq_load = [&](Tile<KIND, KS>& T, int sq) {
+  __shared__ __attribute__((aligned(16))) unsigned char dring[DMA ? NW * P * kTileBytes : 16];
+  unsigned char* const myring = dring + (DMA ? wave * P * kTileBytes : 0);
+  auto seq_load = [&](Tile<KIND, KS>& T, int sq, int slot) {
     const bool past = sq >= ntiles;
     const bool in1 = DOCS == 2 && sq >= nt0;
     // Selects over values: a conditional over the DocRes structs themselves
@@ -231,7 +265,19 @@ stream_fwd_kernel(FwdArgs a) {
     r.rowb = dr0.rowb;
     r.ss = in1 ? dr1.ss : dr0.ss;
     r.sm = in1 ? dr1.sm : dr0.sm;
-    load_tile<KIND, KS, VEC, !GSM, C16, DQ>(T, r, past ? 0 : (in1 ? sq - nt0 : sq), c, g, koff);
+    if constexpr (DMA) {
+      const int tile = past ? 0 : (in1 ? sq - nt0 : sq);
+#pragma unroll
+      for (int k = 0; k < kTileBytes / 1024; ++k) {  // instruction k: rows 4k .. 4k+3
+        const int row = 4 * k + (lane >> 4), col = (lane & 15) ^ row;
+        const uint32_t off = (uint32_t)(tile * 16 + row) * r.rowb + (uint32_t)(col * 16);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            r.d, (__attribute__((address_space(3))) void*)(myring + slot * kTileBytes + k * 1024), 16, off, 0, 0,
+            2 /* nt */);
+      }
+    } else {
+      load_tile<KIND, KS, VEC, !GSM, C16, DQ>(T, r, past ? 0 : (in1 ? sq - nt0 : sq), c, g, koff);
+    }
   };
   // GSM: the scales and mins of a group of P = 4 tiles come with one dword
   // load per array (per doc of the workgroup) instead of two 8-byte loads per
@@ -318,7 +364,10 @@ stream_fwd_kernel(FwdArgs a) {
   // REFILL_ANY loads it whether or not it exists (past the end: the empty
   // range), REFILL_IF only if it exists, REFILL_NONE not at all.
   enum { REFILL_NONE, REFILL_IF, REFILL_ANY };
-  auto process = [&](auto mode_tag, Tile<KIND, KS>& T, int i) __attribute__((always_inline)) {
+  // slot: T's ring position; wait_tag: the vector-memory instructions issued
+  // after this tile's DMA loads (DMA path)
+  auto process = [&](auto mode_tag, Tile<KIND, KS>& T, int i, int slot, auto wait_tag)
+                     __attribute__((always_inline)) {
     constexpr int MODE = decltype(mode_tag)::value;
     const int sq = wave + NW * i;
     const bool in1 = DOCS == 2 && sq >= nt0;
@@ -331,9 +380,18 @@ stream_fwd_kernel(FwdArgs a) {
       cur = 1;
     }
     u32x4_t af[KS];
+    if constexpr (DMA) {
+      // the tile is in LDS once at most wait_tag newer loads are in flight;
+      // its fragments are in registers before the slot is refilled
+      wait_vmem<decltype(wait_tag)::value>();
+#pragma unroll
+      for (int t = 0; t < KS; ++t)
+        af[t] = *reinterpret_cast<const u32x4_t*>(myring + slot * kTileBytes + c * 256 + (((4 * t + g) ^ c) * 16));
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    }
 #pragma unroll
     for (int t = 0; t < KS; ++t) {
-      af[t] = tile_operand<KIND, KS>(T, t);
+      if constexpr (!DMA) af[t] = tile_operand<KIND, KS>(T, t);
       if constexpr (DQ) af[t] = dequant_biased_f16(af[t], T.s[0], T.m[0]);
       if constexpr (KMASK && !U8) {
         if (has_partial && t == tp) af[t] &= pmask;
@@ -346,9 +404,9 @@ stream_fwd_kernel(FwdArgs a) {
     }
     // uint8 codes were converted into registers of their own, so the slot is
     // free; fp16/bf16 MFMAs read the slot itself (the compiler keeps a copy).
-    if constexpr (MODE == REFILL_ANY) seq_load(T, wave + NW * (i + P));
+    if constexpr (MODE == REFILL_ANY) seq_load(T, wave + NW * (i + P), slot);
     if constexpr (MODE == REFILL_IF) {
-      if (i + P < my_n) seq_load(T, wave + NW * (i + P));
+      if (i + P < my_n) seq_load(T, wave + NW * (i + P), slot);
     }
     const int row0 = tile * 16 + 4 * g;
     // S of this tile against every query block, folded into the running
@@ -398,7 +456,7 @@ stream_fwd_kernel(FwdArgs a) {
   uint32_t gsc = 0, gmc = 0, gsn = 0, gmn = 0;  // group scales / mins: current, next
   if constexpr (GSM) group_sm(0, gsc, gmc);
 #pragma unroll
-  for (int s = 0; s < P; ++s) seq_load(buf[s], wave + NW * s);
+  for (int s = 0; s < P; ++s) seq_load(buf[s], wave + NW * s, s);
   q_exchange();
   if constexpr (FIXED) {
     // A fixed load pattern: every group of P tiles that has a next group
@@ -415,23 +473,32 @@ stream_fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int s = 0; s < P; ++s) {
         if constexpr (GSM) tile_sm(buf[s], gsc, gmc, s);
-        process(RefillAny{}, buf[s], i0 + s);
+        // in the steady state P - 1 tiles' loads follow each tile's
+        process(RefillAny{}, buf[s], i0 + s, s, std::integral_constant<int, (kTileBytes / 1024) * (P - 1)>{});
       }
       gsc = gsn;
       gmc = gmn;
     }
-#pragma unroll
-    for (int s = 0; s < P; ++s) {
-      if (i0 + s < my_n) {
-        if constexpr (GSM) tile_sm(buf[s], gsc, gmc, s);
-        process(RefillNone{}, buf[s], i0 + s);
+    // the last group refills nothing: P - 1 - s tiles' loads follow tile s's
+    auto last = [&](auto s_tag) __attribute__((always_inline)) {
+      constexpr int s = decltype(s_tag)::value;
+      if constexpr (s < P) {
+        if (i0 + s < my_n) {
+          if constexpr (GSM) tile_sm(buf[s], gsc, gmc, s);
+          process(RefillNone{}, buf[s], i0 + s, s, std::integral_constant<int, (kTileBytes / 1024) * (P - 1 - s)>{});
+        }
       }
-    }
+    };
+    static_assert(P <= 4, "the last group is unrolled for up to four slots");
+    last(std::integral_constant<int, 0>{});
+    last(std::integral_constant<int, 1>{});
+    last(std::integral_constant<int, 2>{});
+    last(std::integral_constant<int, 3>{});
   } else {
     for (int i0 = 0; i0 < my_n; i0 += P) {
 #pragma unroll
       for (int s = 0; s < P; ++s)
-        if (i0 + s < my_n) process(RefillIf{}, buf[s], i0 + s);
+        if (i0 + s < my_n) process(RefillIf{}, buf[s], i0 + s, s, std::integral_constant<int, 0>{});
     }
   }
 
