@@ -48,16 +48,15 @@ constexpr int stream_depth() {
   return (KIND != KIND_U8 && KS >= 8) ? 2 : 4;
 }
 
-// Doc tiles through a per-wave LDS ring (stream_fwd_kernel's DMA path):
-// fp16/bf16 rows of exactly 128 elements scored without argmax, outside the
-// two-tile ring of short doc pairs (PD = 2). Two tiles in flight per wave
-// (8 KB of LDS each way), so a CU holds three workgroups.
+// Doc tiles through a per-wave LDS ring (stream_fwd_kernel's DMA path) for
+// rows of exactly 128 elements scored without argmax, outside the two-tile
+// ring of short doc pairs (PD = 2): fp16/bf16 with two tiles in flight per
+// wave (8 KB of LDS each), uint8 with the group scale loads' four (2 KB each).
 template <int KIND, int KS, bool KMASK, bool ARGMAX, int PD>
-constexpr bool stream_dma() {
+constexpr bool stream_dma_fp() {
   return KIND != KIND_U8 && KS == 4 && !KMASK && !ARGMAX && PD == 0;
 }
 constexpr int kStreamDmaDepth = 2;
-constexpr int kTileBytes = 16 * 256;  // a DMA tile: 16 rows of 128 fp16/bf16 elements
 
 // Waits until at most N vector-memory instructions of this wave are in
 // flight (vmcnt(N); the other counters at their maxima).
@@ -106,9 +105,10 @@ stream_fwd_kernel(FwdArgs a) {
   // config 1's docs: 60.1 -> 55.5 us with nt). The VGPR ring's loads follow
   // the MFMA fragment order, which touches each line with two instructions;
   // nt made those 17 % slower. Short doc pairs (the PD = 2 ring) keep VGPR
-  // tiles: 5000 docs of 77 tokens 18.3 -> 19.9 us through LDS.
-  constexpr bool DMA = stream_dma<KIND, KS, KMASK, ARGMAX, PD>();
-  constexpr int NW = kStreamWaves, P = PD ? PD : (DMA ? kStreamDmaDepth : stream_depth<KIND, NQB, KS>()),
+  // tiles: 5000 docs of 77 tokens 18.3 -> 19.9 us through LDS. uint8 tiles
+  // take the same path (below).
+  constexpr bool DMA_FP = stream_dma_fp<KIND, KS, KMASK, ARGMAX, PD>();
+  constexpr int NW = kStreamWaves, P = PD ? PD : (DMA_FP ? kStreamDmaDepth : stream_depth<KIND, NQB, KS>()),
                 QROWS = NQB * 16;
   constexpr int ESZ = KindInfo<KIND>::esz;
   constexpr bool BF = KindInfo<KIND>::bf;
@@ -249,9 +249,22 @@ stream_fwd_kernel(FwdArgs a) {
   constexpr bool GSM = U8 && VEC && !DQ && (P == 4 || (P == 2 && JOINT));
   static_assert(!GSM || P == 4 || P == 2, "group scale loads map 16 lanes per tile slot");
   static_assert(!JOINT || DOCS == 2, "a joint scale range serves two-doc group loads");
+  // uint8 DMA tiles: 16 code rows of 128 bytes (two load instructions of 8
+  // rows each), chunk j of row r at j ^ (r % 8); the scales and mins keep the
+  // group loads into registers.
+  // (uint8 queries of up to 32 tokens: config 4 62.2 -> 57.9 us, packed
+  // 64.3 -> 58.6 us; 33-64-token queries lost 5-10 % and keep the VGPR ring)
+  constexpr bool DMA = DMA_FP || (U8 && NQB <= 2 && KS == 4 && !KMASK && !ARGMAX && PD == 0 && GSM);
+  constexpr int RB = U8 ? 128 : 256;       // bytes of a tile row
+  constexpr int TB = 16 * RB;              // bytes of a tile
+  constexpr int TI = TB / 1024;            // DMA instructions per tile
+  constexpr int CPR = RB / 16;             // 16-byte chunks per row
+  // vector-memory instructions between two tiles' DMA loads in the steady
+  // state besides the tiles': a group's scale and min loads
+  constexpr int GL = GSM ? ((JOINT || DOCS == 1) ? 2 : 4) : 0;
   const rsrc_t nul = make_rsrc(a.D, 0u);
-  __shared__ __attribute__((aligned(16))) unsigned char dring[DMA ? NW * P * kTileBytes : 16];
-  unsigned char* const myring = dring + (DMA ? wave * P * kTileBytes : 0);
+  __shared__ __attribute__((aligned(16))) unsigned char dring[DMA ? NW * P * TB : 16];
+  unsigned char* const myring = dring + (DMA ? wave * P * TB : 0);
   auto seq_load = [&](Tile<KIND, KS>& T, int sq, int slot) {
     const bool past = sq >= ntiles;
     const bool in1 = DOCS == 2 && sq >= nt0;
@@ -268,12 +281,11 @@ stream_fwd_kernel(FwdArgs a) {
     if constexpr (DMA) {
       const int tile = past ? 0 : (in1 ? sq - nt0 : sq);
 #pragma unroll
-      for (int k = 0; k < kTileBytes / 1024; ++k) {  // instruction k: rows 4k .. 4k+3
-        const int row = 4 * k + (lane >> 4), col = (lane & 15) ^ row;
+      for (int k = 0; k < TI; ++k) {  // instruction k: rows (1024 / RB) k .. +(1024 / RB) - 1
+        const int row = (1024 / RB) * k + lane / CPR, pos = lane % CPR, col = pos ^ (row % CPR);
         const uint32_t off = (uint32_t)(tile * 16 + row) * r.rowb + (uint32_t)(col * 16);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            r.d, (__attribute__((address_space(3))) void*)(myring + slot * kTileBytes + k * 1024), 16, off, 0, 0,
-            2 /* nt */);
+            r.d, (__attribute__((address_space(3))) void*)(myring + slot * TB + k * 1024), 16, off, 0, 0, 2 /* nt */);
       }
     } else {
       load_tile<KIND, KS, VEC, !GSM, C16, DQ>(T, r, past ? 0 : (in1 ? sq - nt0 : sq), c, g, koff);
@@ -384,14 +396,21 @@ stream_fwd_kernel(FwdArgs a) {
       // the tile is in LDS once at most wait_tag newer loads are in flight;
       // its fragments are in registers before the slot is refilled
       wait_vmem<decltype(wait_tag)::value>();
+      if constexpr (U8) {
+        // codes of k-steps 2h, 2h + 1: bytes 64h + 16g .. +15 of row c (frag_k0)
 #pragma unroll
-      for (int t = 0; t < KS; ++t)
-        af[t] = *reinterpret_cast<const u32x4_t*>(myring + slot * kTileBytes + c * 256 + (((4 * t + g) ^ c) * 16));
+        for (int h = 0; h < KS / 2; ++h)
+          T.v[h] = *reinterpret_cast<const u32x4_t*>(myring + slot * TB + c * RB + (((4 * h + g) ^ (c % CPR)) * 16));
+      } else {
+#pragma unroll
+        for (int t = 0; t < KS; ++t)
+          af[t] = *reinterpret_cast<const u32x4_t*>(myring + slot * TB + c * RB + (((4 * t + g) ^ (c % CPR)) * 16));
+      }
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
     }
 #pragma unroll
     for (int t = 0; t < KS; ++t) {
-      if constexpr (!DMA) af[t] = tile_operand<KIND, KS>(T, t);
+      if constexpr (!DMA_FP) af[t] = tile_operand<KIND, KS>(T, t);
       if constexpr (DQ) af[t] = dequant_biased_f16(af[t], T.s[0], T.m[0]);
       if constexpr (KMASK && !U8) {
         if (has_partial && t == tp) af[t] &= pmask;
@@ -474,7 +493,7 @@ stream_fwd_kernel(FwdArgs a) {
       for (int s = 0; s < P; ++s) {
         if constexpr (GSM) tile_sm(buf[s], gsc, gmc, s);
         // in the steady state P - 1 tiles' loads follow each tile's
-        process(RefillAny{}, buf[s], i0 + s, s, std::integral_constant<int, (kTileBytes / 1024) * (P - 1)>{});
+        process(RefillAny{}, buf[s], i0 + s, s, std::integral_constant<int, TI * (P - 1) + GL>{});
       }
       gsc = gsn;
       gmc = gmn;
@@ -485,7 +504,7 @@ stream_fwd_kernel(FwdArgs a) {
       if constexpr (s < P) {
         if (i0 + s < my_n) {
           if constexpr (GSM) tile_sm(buf[s], gsc, gmc, s);
-          process(RefillNone{}, buf[s], i0 + s, s, std::integral_constant<int, (kTileBytes / 1024) * (P - 1 - s)>{});
+          process(RefillNone{}, buf[s], i0 + s, s, std::integral_constant<int, TI * (P - 1 - s)>{});
         }
       }
     };
@@ -803,7 +822,12 @@ template <int KIND, int NQB, int KS>
 hipError_t dispatch_flags(const FwdArgs& a, bool am, hipStream_t s) {
   if constexpr (KIND == KIND_U8) {
     (void)am;
-    // FwdArgs::vec bit 0: the vector path; bit 1: 16-byte code rows only
+    // FwdArgs::vec bit 0: the vector path; bit 1: 16-byte code rows only.
+    // Rows of exactly 128 codes take the unmasked instance (its doc tiles
+    // come through the LDS ring).
+    if constexpr (KS == 4) {
+      if ((a.vec & 1) && a.d == 128) return launch_one<KIND, NQB, KS, false, false, true>(a, s);
+    }
     if (a.vec & 1) return launch_one<KIND, NQB, KS, true, false, true>(a, s);
     return (a.vec & 2) ? launch_one<KIND, NQB, KS, true, false, false, true>(a, s)
                        : launch_one<KIND, NQB, KS, true, false, false, false>(a, s);
