@@ -69,6 +69,26 @@ __device__ __forceinline__ uint16_t ld2(rsrc_t r, uint32_t voff) {
   return __builtin_amdgcn_raw_buffer_load_b16(r, voff, 0, 0);
 }
 
+// LDS DMA: 16 bytes per lane from the buffer straight into LDS, lane l's at
+// lds + 16 l (lds is wave-uniform), with the non-temporal cache policy. It
+// counts on vmcnt like any buffer load; this wave's LDS reads see the data
+// once vmcnt has dropped past the instruction (wait_vmem below).
+__device__ __forceinline__ void dma16_nt(rsrc_t r, void* lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0,
+                                           2 /* nt */);
+}
+
+// Waits until at most N vector-memory instructions of this wave are in
+// flight (vmcnt(N); the other counters at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+  __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// Waits for this wave's LDS (and scalar-memory) operations (lgkmcnt(0)).
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+
 // Wave-uniform read of an input that no kernel of the launch writes, through
 // the constant address space: the compiler may then use a scalar load, which
 // counts on lgkmcnt. A vector load of it in a kernel that also stores would

@@ -58,14 +58,6 @@ constexpr bool stream_dma_fp() {
 }
 constexpr int kStreamDmaDepth = 2;
 
-// Waits until at most N vector-memory instructions of this wave are in
-// flight (vmcnt(N); the other counters at their maxima).
-template <int N>
-__device__ __forceinline__ void wait_vmem() {
-  static_assert(N >= 0 && N < 64, "vmcnt is six bits");
-  __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
-}
-
 // KMASK: d is not exactly 32*KS, so fragment slots past d must read as zero.
 // VEC: uint8 vector load path (FwdArgs::vec); true for fp16/bf16.
 // DOCS = 2 (one pass, no argmax; uint8 docs of one query, and fp16/bf16 docs
@@ -284,8 +276,7 @@ stream_fwd_kernel(FwdArgs a) {
       for (int k = 0; k < TI; ++k) {  // instruction k: rows (1024 / RB) k .. +(1024 / RB) - 1
         const int row = (1024 / RB) * k + lane / CPR, pos = lane % CPR, col = pos ^ (row % CPR);
         const uint32_t off = (uint32_t)(tile * 16 + row) * r.rowb + (uint32_t)(col * 16);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            r.d, (__attribute__((address_space(3))) void*)(myring + slot * TB + k * 1024), 16, off, 0, 0, 2 /* nt */);
+        dma16_nt(r.d, myring + slot * TB + k * 1024, off);
       }
     } else {
       load_tile<KIND, KS, VEC, !GSM, C16, DQ>(T, r, past ? 0 : (in1 ? sq - nt0 : sq), c, g, koff);
@@ -406,7 +397,7 @@ stream_fwd_kernel(FwdArgs a) {
         for (int t = 0; t < KS; ++t)
           af[t] = *reinterpret_cast<const u32x4_t*>(myring + slot * TB + c * RB + (((4 * t + g) ^ (c % CPR)) * 16));
       }
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      wait_lds();
     }
 #pragma unroll
     for (int t = 0; t < KS; ++t) {

@@ -168,12 +168,17 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
   // stores cost more than the deeper ring gains (Nq = 8 x 32: +3 %).
   // uint8 docs (single queries, no argmax) always stage through VGPRs, where
   // each chunk of eight codes is dequantised to fp16 on its way to LDS; the
-  // MFMA and everything after it are the fp16 kernel's.
+  // MFMA and everything after it are the fp16 kernel's. Their row blocks of
+  // up to 32 rows per wave take the register ring too, whose barrier leaves
+  // the ring's loads in flight where the plain staging loop's workgroup fence
+  // drains them every tile (128-token query over 5000 docs of 77 tokens
+  // 28.3 -> 25.7 us, 200 tokens over 2000 docs of 300: 45.3 -> 41.3 us);
+  // with 64 rows per wave the ring spills.
   constexpr bool U8 = KIND == KIND_U8;
   static_assert(!(U8 && ARGMAX), "uint8 docs are scored without argmax");
   constexpr int ESZ = KindInfo<KIND>::esz;
   using stage_t = std::conditional_t<U8, U8Chunk, u32x4_t>;
-  constexpr bool RING = !ARGMAX && NB == 1 && KS == 4;
+  constexpr bool RING = !ARGMAX && KS == 4 && (NB == 1 || (U8 && NB <= 2));
   constexpr int PR = 4;
   constexpr bool DMA = !KMASK && !ARGMAX && !RING && !U8;
   constexpr int ROWB = 64 * KS + (DMA ? 0 : 16);  // LDS bytes per token row

@@ -41,7 +41,11 @@ __device__ __forceinline__ float src_elem(const void* p, int64_t i) {
 
 // Eight consecutive source elements k0..k0+7 of a row; elements at or past d
 // are not read (they come back as 0 and are excluded by the caller).
-template <int SRC>
+// NT: the 16-byte loads are non-temporal, for fp16/bf16 rows of 64 elements
+// or more, where every load instruction of a wave covers whole 128-byte lines
+// and the source is read once (config 4's docs 389 -> 385 us); the
+// non-temporal policy costs where an instruction covers half lines.
+template <int SRC, bool NT>
 __device__ __forceinline__ void load8(const void* row, int k0, int d, bool vec, float (&x)[8]) {
   if (vec && k0 + 8 <= d) {
     if constexpr (SRC == 2) {
@@ -53,7 +57,8 @@ __device__ __forceinline__ void load8(const void* row, int k0, int d, bool vec, 
         x[4 + i] = b[i];
       }
     } else {
-      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(row) + k0);
+      const u32x4_t* p = reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(row) + k0);
+      const u32x4_t v = NT ? __builtin_nontemporal_load(p) : *p;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         if constexpr (SRC == 0) {
@@ -145,7 +150,8 @@ __global__ void __launch_bounds__(256) quantize_kernel(QuantArgs a) {
       if (j < jend && j < len) {
         const char* src = static_cast<const char*>(a.src) + (b * a.s_stride_b + j * a.s_stride_l) * a.esz;
 #pragma unroll
-        for (int cc = 0; cc < CPL; ++cc) load8<SRC>(src, (cc * LPR + lane_in_row) * 8, a.d, a.vec != 0, x[k][cc]);
+        for (int cc = 0; cc < CPL; ++cc)
+          load8<SRC, (SRC != 2 && LPR >= 8)>(src, (cc * LPR + lane_in_row) * 8, a.d, a.vec != 0, x[k][cc]);
       }
     }
 #pragma unroll
