@@ -171,6 +171,7 @@ __global__ void __launch_bounds__(256) bwd_dq_finalize_kernel(BwdArgs a) {
 
 constexpr int kEntryBits = 13;  // entries of one chunk < 2^13 (kDdChunk)
 constexpr uint32_t kNoRow = 0xffffffffu;
+constexpr int kDdMaxPasses = 4;  // workgroup row passes per dD writer slab, at most
 
 // dD index, one workgroup per (doc, chunk of kDdChunk consecutive (query,
 // token) entries). The chunk's entries e become keys row << 13 | (e - e0) in
@@ -258,9 +259,19 @@ __device__ __forceinline__ void dd_write_block(const BwdArgs& a, int slab) {
   const int NL = a.Nq * a.Lq;
   const uint16_t* Q = static_cast<const uint16_t*>(a.Q);
   const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (; r < r1; r += step) {
+  // The row-index entries of all of this lane's passes (a slab is at most
+  // kDdMaxPasses of them) are loaded up front, so their round trips overlap.
+  uint32_t infos[kDdMaxPasses];
+#pragma unroll
+  for (int p = 0; p < kDdMaxPasses; ++p) {
+    const int64_t rp = r + (int64_t)p * step;
+    infos[p] = rp < r1 ? a.dd_rows[rp] : kNoRow;
+  }
+#pragma unroll
+  for (int p = 0; p < kDdMaxPasses; ++p, r += step) {
+    if (r >= r1) break;
     uint16_t* orow = static_cast<uint16_t*>(a.dD) + r * a.d;
-    const uint32_t info0 = a.dd_rows[r];
+    const uint32_t info0 = infos[p];
     if (a.dd_chunks == 1 && info0 == kNoRow) {
       for (int kc = kc0; kc < nkc; kc += 64) store8<BF>(orow, kc * 8, a.d, zero);
     } else {
@@ -370,7 +381,8 @@ size_t bwd_dd_index_bytes(int64_t B, int64_t entries, int64_t Ld) {
 }
 
 // Rows per dD writer workgroup: about 16 KB of output, a whole number of
-// the workgroup's row passes (4 waves x 64 / L rows, L lanes per row).
+// the workgroup's row passes (4 waves x 64 / L rows, L lanes per row), at
+// most kDdMaxPasses of them.
 int bwd_dd_slab(int d) {
   const int nkc = (d + 7) / 8;
   int lsh = 0;
@@ -378,6 +390,7 @@ int bwd_dd_slab(int d) {
   const int pass = 4 * (64 >> lsh);
   int rows = 16384 / (2 * d);
   if (rows < pass) rows = pass;
+  if (rows > kDdMaxPasses * pass) rows = kDdMaxPasses * pass;
   return (rows + pass - 1) / pass * pass;
 }
 
