@@ -97,6 +97,17 @@ __device__ __forceinline__ float div_rn(float a, float b, float y) {
   return __builtin_fmaf(rem, y, q1);
 }
 
+// Byte `sel` of `into` replaced by q rounded half to even and clamped to
+// [0, 255], NaN giving 0: torch's round() then clamp(0, 255) and the uint8
+// cast in one v_cvt_pk_u8_f32 (in the default round-to-nearest-even mode, the
+// conversion saturates and sends NaN to 0; checked on gfx950 against rint and
+// clamp over every half-integer from 0.5 to 256.5 and its two neighbours,
+// -4 .. 300 in steps of 1/8, +-inf, +-0 and NaN; the quantiser's bit-exact
+// tests cover quotients on and next to half-integers).
+__device__ __forceinline__ uint32_t cvt_u8_rne(float q, int sel, uint32_t into) {
+  return __builtin_amdgcn_cvt_pk_u8_f32(q, sel, into);
+}
+
 template <bool MAX>
 __device__ __forceinline__ float mm(float a, float b) {  // NaN-propagating, as torch.aminmax
   return MAX ? __builtin_elementwise_maximum(a, b) : __builtin_elementwise_minimum(a, b);
@@ -202,10 +213,7 @@ __global__ void __launch_bounds__(256) quantize_kernel(QuantArgs a) {
         uint32_t w[2] = {0u, 0u};
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          float v = __builtin_rintf(div_rn<SRC == 0>(x[k][cc][i] - lo, step, rstep));
-          v = fminf(fmaxf(v, 0.f), 255.f);  // NaN -> 0 (fmaxf returns the number)
-          // v is an integer in [0, 255]: the byte conversion is exact.
-          w[i >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(v, i & 3, w[i >> 2]);
+          w[i >> 2] = cvt_u8_rne(div_rn<SRC == 0>(x[k][cc][i] - lo, step, rstep), i & 3, w[i >> 2]);
         }
         if (a.vec && k0 + 8 <= a.d) {
           // non-temporal: the codes are read by a later scoring call, not by
@@ -296,9 +304,7 @@ __global__ void __launch_bounds__(256) quantize_wide_kernel(QuantArgs a) {
     if (step < 1e-8f) step = 1e-8f;
     const float rstep = 1.0f / step;
     for (int64_t k = tid; k < a.d; k += 256) {
-      float v = __builtin_rintf(div_rn<SRC == 0>(src_elem<SRC>(src, k) - lo, step, rstep));
-      v = fminf(fmaxf(v, 0.f), 255.f);
-      crow[k] = (uint8_t)v;
+      crow[k] = (uint8_t)cvt_u8_rne(div_rn<SRC == 0>(src_elem<SRC>(src, k) - lo, step, rstep), 0, 0u);
     }
     if (tid == 0) {
       *sp = __builtin_bit_cast(uint16_t, (_Float16)step);
