@@ -57,6 +57,8 @@ constexpr bool stream_dma_fp() {
   return KIND != KIND_U8 && KS == 4 && !KMASK && !ARGMAX && PD == 0;
 }
 constexpr int kStreamDmaDepth = 2;
+// uint8 docs take the LDS ring from this many code bytes (docs x Ld x d).
+constexpr int64_t kU8RingMinBytes = (int64_t)1 << 28;
 
 // KMASK: d is not exactly 32*KS, so fragment slots past d must read as zero.
 // VEC: uint8 vector load path (FwdArgs::vec); true for fp16/bf16.
@@ -84,7 +86,7 @@ constexpr int stream_min_waves() {
 
 // PD: ring depth other than stream_depth's (0: stream_depth's).
 template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX, bool VEC, int DOCS = 1, bool JOINT = false, int PD = 0,
-          bool C16 = VEC>
+          bool C16 = VEC, bool U8RING = true>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(stream_min_waves<KIND, NQB, KS, VEC, DOCS>())))
 stream_fwd_kernel(FwdArgs a) {
   // DMA: each wave's ring lives in LDS. A tile's 16 rows of 256 bytes come by
@@ -245,8 +247,10 @@ stream_fwd_kernel(FwdArgs a) {
   // rows each), chunk j of row r at j ^ (r % 8); the scales and mins keep the
   // group loads into registers.
   // (uint8 queries of up to 32 tokens: config 4 62.2 -> 57.9 us, packed
-  // 64.3 -> 58.6 us; 33-64-token queries lost 5-10 % and keep the VGPR ring)
-  constexpr bool DMA = DMA_FP || (U8 && NQB <= 2 && KS == 4 && !KMASK && !ARGMAX && PD == 0 && GSM);
+  // 64.3 -> 58.6 us; 33-64-token queries lost 5-10 % and keep the VGPR ring).
+  // U8RING = false keeps the VGPR ring for smaller uint8 workloads (the
+  // launch's choice, kU8RingMinBytes).
+  constexpr bool DMA = DMA_FP || (U8RING && U8 && NQB <= 2 && KS == 4 && !KMASK && !ARGMAX && PD == 0 && GSM);
   constexpr int RB = U8 ? 128 : 256;       // bytes of a tile row
   constexpr int TB = 16 * RB;              // bytes of a tile
   constexpr int TI = TB / 1024;            // DMA instructions per tile
@@ -764,7 +768,24 @@ hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
                              0, s, a);
         }
       } else if (GROUPS && sm_rows * 2 + 64 < ((int64_t)1 << 31)) {
-        hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2, GROUPS>), grid, dim3(256), 0, s, a);
+        // The LDS ring (queries of up to 32 tokens, d = 128) takes 32 KB of
+        // LDS per workgroup, four workgroups per CU against eight: it pays
+        // once the stream is long, and costs where start-up and the last
+        // round of workgroups weigh more (1000-10000 docs of 300-1024 tokens,
+        // ring against VGPR ring: 300 tokens 16.0 / 32.0 / 67.6 against
+        // 17.0 / 36.1 / 67.7 us, 512 tokens 22.3 / 57.5 / 112.0 against
+        // 26.2 / 54.3 / 100.7 us, 1024 tokens 40.7 / 111.8 / 217.8 against
+        // 45.1 / 100.0 / 194.5 us for 2000 / 5000 / 10000 docs; config 4
+        // 61.5 against 57.9 us).
+        bool ring = true;
+        if constexpr (NQB <= 2 && KS == 4 && !KMASK) ring = items * a.Ld * a.d >= kU8RingMinBytes;
+        if (ring) {
+          hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2, GROUPS>), grid, dim3(256), 0, s,
+                             a);
+        } else {
+          hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2, GROUPS, 0, VEC, false>), grid,
+                             dim3(256), 0, s, a);
+        }
       } else {
         hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2, false, 0, C16>), grid, dim3(256), 0,
                            s, a);

@@ -72,6 +72,31 @@ def test_config4_full_size(oracle_mod):
     assert abs(float(odd[4998]) - ref[pick.index(4998)]) <= ATOL
 
 
+def test_u8_lds_ring_and_vgpr_ring_agree(oracle_mod):
+    """uint8 docs of a 32-token query at d = 128 stream through the LDS ring
+    from 2^28 code bytes (docs x Ld x d) and through the VGPR ring below; both
+    feed the MFMAs the same fragments in the same order. 2200 docs of 1024
+    tokens (288 MB: LDS ring) must score bit-identically to the same docs in
+    batches of 1000 (131 MB: VGPR ring), with empty, one-token, tile-edge and
+    full-length docs on both sides of a pair; sampled docs against the oracle."""
+    B = 2200
+    Q = sim((32, 128), 45)
+    codes, scales, mins = _config4_docs(B)
+    lengths = torch.randint(0, 1025, (B,), generator=torch.Generator().manual_seed(46), dtype=torch.int32)
+    edge = {0: 0, 1: 1, 2: 15, 3: 16, 4: 17, 5: 1024, 998: 0, 999: 1024, 1000: 1, 1001: 0, 2198: 33, 2199: 1023}
+    for b, n in edge.items():
+        lengths[b] = n
+    Qd, ld = Q.to(DEV), lengths.to(DEV)
+    whole = fm.flash_maxsim_int8(Qd, codes, scales, mins, ld).cpu()
+    parts = torch.cat([fm.flash_maxsim_int8(Qd, codes[b0:b0 + 1000], scales[b0:b0 + 1000], mins[b0:b0 + 1000],
+                                            ld[b0:b0 + 1000]).cpu() for b0 in range(0, B, 1000)])
+    assert torch.equal(whole, parts)
+    pick = sorted(set(sample_docs(B, 16, 5)) | set(edge))
+    ref = oracle_mod.maxsim_int8(to_np32(Q), codes[pick].cpu().numpy(), to_np32(scales[pick]),
+                                 to_np32(mins[pick]), lengths[pick].numpy())
+    assert_scores(whole[pick], ref)
+
+
 def test_per_query_docs_bench_shape(oracle_mod):
     """shared_docs=False at Q[100,32,128] x D[100,50,300,128] (reference
     flash_maxsim.py:241-244): 3 whole queries plus 300 sampled pairs."""
