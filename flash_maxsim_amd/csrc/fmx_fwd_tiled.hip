@@ -193,8 +193,15 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
   // a ds_read of one buffer cannot alias the DMA writes in flight to the
   // other, and places no wait for those writes in front of it.
   // The staging path keeps both buffers in one array indexed at run time.
+  // DMA3: a third buffer (two tiles in flight) for eight-wave blocks, where
+  // the workgroups per CU still fit the CU's 160 KB with it (config 3 900 ->
+  // 889 us, config 2 172.7 -> 171.6 us; four-wave blocks of 128 rows lost
+  // 2-3 %: their three workgroups per CU already overlap the tile loads).
+  constexpr int RMB = 2 * (ARGMAX ? 1 : 4) * NW * NB * 16 * 4;  // bytes of the row-maxima buffers
+  constexpr bool DMA3 = DMA && NW == 8 && tiled_wpc(NW, NB, KS) * (3 * BUFB + RMB) <= 160 * 1024;
   __shared__ __attribute__((aligned(16))) unsigned char lds0[DMA ? BUFB : 16];
   __shared__ __attribute__((aligned(16))) unsigned char lds1[DMA ? BUFB : 16];
+  __shared__ __attribute__((aligned(16))) unsigned char lds2[DMA3 ? BUFB : 16];
   __shared__ __attribute__((aligned(16))) unsigned char ldsa[DMA ? 16 : 2 * BUFB];
   // Row maxima of a finished doc (double-buffered by doc parity). Scores:
   // the four row groups' maxima of each row side by side (RG = 4), merged by
@@ -553,6 +560,57 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
     using S3 = std::integral_constant<int, 3 % PR>;
     static_assert(PR == 4, "the unrolled walk below names four slots");
     while (step(S0{}) && step(S1{}) && step(S2{}) && step(S3{})) {
+    }
+  } else if constexpr (DMA3) {
+    // Three buffers, two tiles in flight: tile j of the walk lands in buffer
+    // j % 3. While tile j computes, tile j + 2's loads go into the buffer tile
+    // j - 1 was read from (before the previous barrier), and the barrier
+    // waits only for tile j + 1 (vmcnt(CPT): tile j + 2's CPT load
+    // instructions may stay in flight). A prefetch cursor (pb, pt) runs two
+    // tiles ahead; past the end of the walk it loads from an empty range
+    // (zeros into LDS, no memory access), so every step issues the same loads.
+    int pb = b, pt = 0, pnt = nt;
+    TileRes prd = rd;
+    const rsrc_t z = make_rsrc(a.D, 0u);
+    auto issue = [&](unsigned char* dst) __attribute__((always_inline)) {
+      const bool have = pb < a.B;
+      const TileRes r = {have ? prd.d : z, z, z};
+      dma_tile(r, have ? pt : 0, dst);
+      if (!have) return;
+      if (++pt >= pnt) {
+        pb += G;
+        pt = 0;
+        if (pb < a.B) {
+          const int l = doc_len(pb);
+          pnt = l > 0 ? (l + TJ - 1) / TJ : 1;
+          prd = tile_rsrc(pb, l);
+        }
+      }
+    };
+    issue(lds0);
+    issue(lds1);
+    wait_vmem<CPT>();  // tile 0 is in LDS; tile 1 may be in flight
+    barrier_lds();
+    auto step = [&](unsigned char* const cur, unsigned char* const ahead) __attribute__((always_inline)) -> bool {
+      issue(ahead);
+      compute_tile(cur);
+      const bool last = t + 1 >= nt;
+      if (last) finish_doc();
+      wait_vmem<CPT>();  // this wave's loads of the next tile are in LDS
+      barrier_lds();     // so are every wave's; every wave is done with cur
+      if (last) doc_sums();
+      if (last) {
+        b += G;
+        if (b >= a.B) return false;
+        len = doc_len(b);
+        nt = len > 0 ? (len + TJ - 1) / TJ : 1;
+        t = 0;
+      } else {
+        ++t;
+      }
+      return true;
+    };
+    while (step(lds0, lds2) && step(lds1, lds0) && step(lds2, lds1)) {
     }
   } else if constexpr (DMA) {
     dma_tile(rd, 0, lds0);
