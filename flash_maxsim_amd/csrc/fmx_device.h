@@ -70,12 +70,14 @@ __device__ __forceinline__ uint16_t ld2(rsrc_t r, uint32_t voff) {
 }
 
 // LDS DMA: 16 bytes per lane from the buffer straight into LDS, lane l's at
-// lds + 16 l (lds is wave-uniform), with the non-temporal cache policy. It
-// counts on vmcnt like any buffer load; this wave's LDS reads see the data
-// once vmcnt has dropped past the instruction (wait_vmem below).
-__device__ __forceinline__ void dma16_nt(rsrc_t r, void* lds, uint32_t voff) {
+// lds + 16 l (lds is wave-uniform); NT: with the non-temporal cache policy
+// (the lines are not kept in the caches), else the default one. It counts on
+// vmcnt like any buffer load; this wave's LDS reads see the data once vmcnt
+// has dropped past the instruction (wait_vmem below).
+template <bool NT>
+__device__ __forceinline__ void dma16_lds(rsrc_t r, void* lds, uint32_t voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0,
-                                           2 /* nt */);
+                                           NT ? 2 : 0);
 }
 
 // Waits until at most N vector-memory instructions of this wave are in

@@ -57,8 +57,16 @@ constexpr bool stream_dma_fp() {
   return KIND != KIND_U8 && KS == 4 && !KMASK && !ARGMAX && PD == 0;
 }
 constexpr int kStreamDmaDepth = 2;
-// uint8 docs take the LDS ring from this many code bytes (docs x Ld x d).
-constexpr int64_t kU8RingMinBytes = (int64_t)1 << 28;
+// Docs of this many bytes or more (docs x Ld x d x element size) outgrow the
+// 256 MB last-level cache: their LDS ring loads are non-temporal, and uint8
+// docs take the LDS ring only from here. Smaller doc sets, scored again by
+// the next call, are read with the default policy and stay in that cache.
+constexpr int64_t kLlcBytes = (int64_t)1 << 28;
+
+int64_t stream_doc_bytes(const FwdArgs& a, int esz) {
+  const int64_t rows = a.tok_group ? a.tok_rows : (int64_t)(a.shared_docs ? 1 : a.Nq) * a.B * a.Ld;
+  return rows * a.d * esz;
+}
 
 // KMASK: d is not exactly 32*KS, so fragment slots past d must read as zero.
 // VEC: uint8 vector load path (FwdArgs::vec); true for fp16/bf16.
@@ -86,7 +94,7 @@ constexpr int stream_min_waves() {
 
 // PD: ring depth other than stream_depth's (0: stream_depth's).
 template <int KIND, int NQB, int KS, bool KMASK, bool ARGMAX, bool VEC, int DOCS = 1, bool JOINT = false, int PD = 0,
-          bool C16 = VEC, bool U8RING = true>
+          bool C16 = VEC, bool U8RING = true, bool NT = true>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(stream_min_waves<KIND, NQB, KS, VEC, DOCS>())))
 stream_fwd_kernel(FwdArgs a) {
   // DMA: each wave's ring lives in LDS. A tile's 16 rows of 256 bytes come by
@@ -248,8 +256,9 @@ stream_fwd_kernel(FwdArgs a) {
   // group loads into registers.
   // (uint8 queries of up to 32 tokens: config 4 62.2 -> 57.9 us, packed
   // 64.3 -> 58.6 us; 33-64-token queries lost 5-10 % and keep the VGPR ring).
-  // U8RING = false keeps the VGPR ring for smaller uint8 workloads (the
-  // launch's choice, kU8RingMinBytes).
+  // U8RING = false keeps the VGPR ring for smaller uint8 workloads, and
+  // NT = false takes the default cache policy for smaller fp16/bf16 doc sets
+  // (the launch's choices, kLlcBytes).
   constexpr bool DMA = DMA_FP || (U8RING && U8 && NQB <= 2 && KS == 4 && !KMASK && !ARGMAX && PD == 0 && GSM);
   constexpr int RB = U8 ? 128 : 256;       // bytes of a tile row
   constexpr int TB = 16 * RB;              // bytes of a tile
@@ -280,7 +289,7 @@ stream_fwd_kernel(FwdArgs a) {
       for (int k = 0; k < TI; ++k) {  // instruction k: rows (1024 / RB) k .. +(1024 / RB) - 1
         const int row = (1024 / RB) * k + lane / CPR, pos = lane % CPR, col = pos ^ (row % CPR);
         const uint32_t off = (uint32_t)(tile * 16 + row) * r.rowb + (uint32_t)(col * 16);
-        dma16_nt(r.d, myring + slot * TB + k * 1024, off);
+        dma16_lds<NT>(r.d, myring + slot * TB + k * 1024, off);
       }
     } else {
       load_tile<KIND, KS, VEC, !GSM, C16, DQ>(T, r, past ? 0 : (in1 ? sq - nt0 : sq), c, g, koff);
@@ -602,7 +611,11 @@ __global__ void __launch_bounds__(256) sum_passes_kernel(FwdArgs a, int npass) {
 // (its cursor arithmetic cost more than the shared ring saved).
 constexpr int kShRow = 272;  // LDS bytes per dequantised token row; 256 + 16 spreads a b128 read's lanes over all banks
 
-template <int P>
+// NT: the code loads (four whole 128-byte rows per wave instruction) are
+// non-temporal, for doc sets past the last-level cache (kLlcBytes: config 4's
+// docs 105.9 -> 101.8 us, 5000 docs of 512 tokens 96.6 -> 94.0 us; smaller
+// sets lost up to 13 % with it, no longer found in that cache by the next call).
+template <int P, bool NT>
 __global__ void __launch_bounds__(256) stream_u8_shared_kernel(FwdArgs a) {
   static_assert(kStreamWaves == 4, "four waves of 32 query rows and 4 tile tokens each");
   __shared__ __attribute__((aligned(16))) unsigned char tl[2][16 * kShRow];
@@ -644,7 +657,7 @@ __global__ void __launch_bounds__(256) stream_u8_shared_kernel(FwdArgs a) {
     int row = tile * 16 + r0;
     row = row < rlast ? row : rlast;
     const bool past = tile >= nt;  // the empty range: no access, a fixed load count
-    S.v = ld8(past ? nul : dr.d, (uint32_t)row * dr.rowb + kb);
+    S.v = __builtin_amdgcn_raw_buffer_load_b64(past ? nul : dr.d, (uint32_t)row * dr.rowb + kb, 0, NT ? 2 : 0);
     S.s = ld2(past ? nul : dr.s, (uint32_t)row * 2u);
     S.m = ld2(past ? nul : dr.m, (uint32_t)row * 2u);
   };
@@ -735,7 +748,11 @@ hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
     // d in (64, 128] and 65-128 query tokens over padded docs: the shared-tile kernel.
     if constexpr (NQB == 8 && KS == 4 && VEC) {
       if (a.Nq == 1 && npass == 1 && !a.qidx && !a.tok_group) {
-        hipLaunchKernelGGL((stream_u8_shared_kernel<4>), dim3((unsigned)a.B), dim3(256), 0, s, a);
+        if (stream_doc_bytes(a, 1) >= kLlcBytes) {
+          hipLaunchKernelGGL((stream_u8_shared_kernel<4, true>), dim3((unsigned)a.B), dim3(256), 0, s, a);
+        } else {
+          hipLaunchKernelGGL((stream_u8_shared_kernel<4, false>), dim3((unsigned)a.B), dim3(256), 0, s, a);
+        }
         return hipGetLastError();
       }
     }
@@ -778,7 +795,7 @@ hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
         // 45.1 / 100.0 / 194.5 us for 2000 / 5000 / 10000 docs; config 4
         // 61.5 against 57.9 us).
         bool ring = true;
-        if constexpr (NQB <= 2 && KS == 4 && !KMASK) ring = items * a.Ld * a.d >= kU8RingMinBytes;
+        if constexpr (NQB <= 2 && KS == 4 && !KMASK) ring = stream_doc_bytes(a, 1) >= kLlcBytes;
         if (ring) {
           hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2, GROUPS>), grid, dim3(256), 0, s,
                              a);
@@ -816,14 +833,31 @@ hipError_t launch_one(const FwdArgs& a, hipStream_t s) {
       return hipGetLastError();
     }
     if ((a.Nq == 1 || !a.shared_docs) && npass == 1 && !a.qidx && (BIG ? !KMASK : a.Ld <= 256)) {
-      hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2>),
-                         dim3((unsigned)(a.Nq * ((a.B + 1) / 2))), dim3(256), 0, s, a);
+      const dim3 grid((unsigned)(a.Nq * ((a.B + 1) / 2)));
+      if constexpr (stream_dma_fp<KIND, KS, KMASK, ARGMAX, 0>()) {
+        if (stream_doc_bytes(a, 2) < kLlcBytes) {  // cached doc sets: the default policy
+          hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2, false, 0, VEC, true, false>),
+                             grid, dim3(256), 0, s, a);
+          return hipGetLastError();
+        }
+      }
+      hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 2>), grid, dim3(256), 0, s, a);
       return hipGetLastError();
     }
   }
   const int64_t grid = npass > 1 ? ((items + 7) / 8) * 8 * npass : items;
-  hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 1, false, 0, C16>), dim3((unsigned)grid),
-                     dim3(256), 0, s, a);
+  bool cached = false;  // a doc set the last-level cache holds: the LDS ring's default policy
+  if constexpr (stream_dma_fp<KIND, KS, KMASK, ARGMAX, 0>()) cached = stream_doc_bytes(a, KindInfo<KIND>::esz) < kLlcBytes;
+  if constexpr (stream_dma_fp<KIND, KS, KMASK, ARGMAX, 0>()) {
+    if (cached) {
+      hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 1, false, 0, C16, true, false>),
+                         dim3((unsigned)grid), dim3(256), 0, s, a);
+    }
+  }
+  if (!cached) {
+    hipLaunchKernelGGL((stream_fwd_kernel<KIND, NQB, KS, KMASK, ARGMAX, VEC, 1, false, 0, C16>), dim3((unsigned)grid),
+                       dim3(256), 0, s, a);
+  }
   if (npass > 1) {
     hipLaunchKernelGGL(sum_passes_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, a, npass);
   }

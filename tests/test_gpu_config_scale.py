@@ -75,7 +75,8 @@ def test_config4_full_size(oracle_mod):
 def test_u8_lds_ring_and_vgpr_ring_agree(oracle_mod):
     """uint8 docs of a 32-token query at d = 128 stream through the LDS ring
     from 2^28 code bytes (docs x Ld x d) and through the VGPR ring below; both
-    feed the MFMAs the same fragments in the same order. 2200 docs of 1024
+    feed the MFMAs the same fragments in the same order (and a 128-token query
+    reads the codes with the non-temporal policy from that size). 2200 docs of 1024
     tokens (288 MB: LDS ring) must score bit-identically to the same docs in
     batches of 1000 (131 MB: VGPR ring), with empty, one-token, tile-edge and
     full-length docs on both sides of a pair; sampled docs against the oracle."""
@@ -95,6 +96,13 @@ def test_u8_lds_ring_and_vgpr_ring_agree(oracle_mod):
     ref = oracle_mod.maxsim_int8(to_np32(Q), codes[pick].cpu().numpy(), to_np32(scales[pick]),
                                  to_np32(mins[pick]), lengths[pick].numpy())
     assert_scores(whole[pick], ref)
+    # a 128-token query on the shared-tile kernel, whose code loads take the
+    # non-temporal policy from the same size: both policies, same scores
+    Q2 = sim((128, 128), 47).to(DEV)
+    whole2 = fm.flash_maxsim_int8(Q2, codes, scales, mins, ld).cpu()
+    parts2 = torch.cat([fm.flash_maxsim_int8(Q2, codes[b0:b0 + 1000], scales[b0:b0 + 1000], mins[b0:b0 + 1000],
+                                             ld[b0:b0 + 1000]).cpu() for b0 in range(0, B, 1000)])
+    assert torch.equal(whole2, parts2)
 
 
 def test_per_query_docs_bench_shape(oracle_mod):
