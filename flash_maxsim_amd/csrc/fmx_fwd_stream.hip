@@ -100,7 +100,7 @@ stream_fwd_kernel(FwdArgs a) {
   // DMA: each wave's ring lives in LDS. A tile's 16 rows of 256 bytes come by
   // LDS DMA loads of whole 128-byte lines (four rows per instruction, 16-byte
   // chunks swizzled by row, chunk j of row r at j ^ r, so the fragment reads
-  // spread over all banks) with the nt cache policy, and the MFMA fragments
+  // spread over all banks) with the nt cache policy (NT), and the MFMA fragments
   // are read from LDS. With whole lines per load instruction the nt policy
   // streams them: config 1 60.8 -> 55.2 us, per-query docs 61.7 -> 56.0 us,
   // Q[128,128] over 1000 docs of 1024 tokens 46.8 -> 44.1 us (a plain read of
@@ -108,7 +108,9 @@ stream_fwd_kernel(FwdArgs a) {
   // the MFMA fragment order, which touches each line with two instructions;
   // nt made those 17 % slower. Short doc pairs (the PD = 2 ring) keep VGPR
   // tiles: 5000 docs of 77 tokens 18.3 -> 19.9 us through LDS. uint8 tiles
-  // take the same path (below).
+  // take the same path (below). NT = false: the default cache policy, for doc
+  // sets the last-level cache holds (kLlcBytes; the medium row, 262 MB:
+  // 44.3 -> 41.9 us).
   constexpr bool DMA_FP = stream_dma_fp<KIND, KS, KMASK, ARGMAX, PD>();
   constexpr int NW = kStreamWaves, P = PD ? PD : (DMA_FP ? kStreamDmaDepth : stream_depth<KIND, NQB, KS>()),
                 QROWS = NQB * 16;
