@@ -27,7 +27,7 @@
 namespace fmx {
 namespace {
 
-constexpr int kWideQB = 8;     // 16-token query blocks per similarity pass
+constexpr int kWideQB = 8;     // 16-token query blocks per similarity pass, at most
 constexpr int kWideTW = 2;     // 16-token doc tiles per wave
 constexpr int kWideKC = 4;     // k-steps per staged query chunk
 constexpr int kWideQRow = 80;  // LDS bytes per query row and k-step: 64 + 16 spreads a b128 read over all banks
@@ -42,16 +42,20 @@ __device__ __forceinline__ void wide_item(const FwdArgs& a, int item, int& qi, i
 }
 
 // blockIdx.x: item of the chunk; blockIdx.y: group of 4 * kWideTW doc tiles;
-// blockIdx.z: group of kWideQB query blocks. S rows are ldp floats apart.
-// The workgroup's 128 query rows come through LDS kWideKC k-steps at a time
-// (each thread loads 16 bytes of two rows per k-step), so L2 serves each
-// query fragment once per workgroup instead of once per wave; the next
+// blockIdx.z: group of QB query blocks. S rows are ldp floats apart.
+// The workgroup's 16 * QB query rows come through LDS kWideKC k-steps at a
+// time (each thread loads 16 bytes of up to two rows per k-step), so L2 serves
+// each query fragment once per workgroup instead of once per wave; the next
 // chunk's query and doc fragments are loaded while this chunk's MFMAs run.
-template <int KIND>
+// QB (2, 4 or 8) follows the query: a 32-token query's accumulators and
+// staging take a quarter of the 128-row instance's registers and LDS, so more
+// waves share a CU.
+template <int KIND, int QB>
 __global__ void __launch_bounds__(256) wide_sim_kernel(FwdArgs a, float* S, int item0, int ldp) {
   constexpr bool U8 = KIND == KIND_U8;
   constexpr int ESZ = KindInfo<KIND>::esz;
-  __shared__ __attribute__((aligned(16))) unsigned char qs[kWideKC][16 * kWideQB * kWideQRow];
+  constexpr int NH = (16 * QB + 63) / 64;  // staged rows per thread and k-step
+  __shared__ __attribute__((aligned(16))) unsigned char qs[kWideKC][16 * QB * kWideQRow];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 15, g = lane >> 4;
@@ -62,25 +66,25 @@ __global__ void __launch_bounds__(256) wide_sim_kernel(FwdArgs a, float* S, int 
   if (blockIdx.y * 4 * kWideTW * 16 >= len) return;  // the whole workgroup: before any barrier
   const int tile0 = (blockIdx.y * 4 + wave) * kWideTW;
   const bool active = tile0 * 16 < len;  // wave-uniform; inactive waves still stage query rows
-  const int qb0 = blockIdx.z * kWideQB;
-  const int nqb = (a.Lq + 15) / 16 - qb0 < kWideQB ? (a.Lq + 15) / 16 - qb0 : kWideQB;
+  const int qb0 = blockIdx.z * QB;
+  const int nqb = (a.Lq + 15) / 16 - qb0 < QB ? (a.Lq + 15) / 16 - qb0 : QB;
   const int kp = a.d & ~7;
   const u32x4_t pmask = prefix_mask16(a.d & 7);
 
   // query staging: thread (r, p) = (tid / 4, tid % 4) loads bytes 16p .. 16p+15 of
-  // each k-step of rows r and r + 64 of the block group
+  // each k-step of rows r (and r + 64) of the block group
   const rsrc_t rq = make_rsrc((const char*)a.Q + (int64_t)qi * a.sq_n * 2, (uint32_t)(a.Lq_rows * a.sq_l * 2));
   const int sr = tid >> 2, sp = tid & 3;
-  uint32_t qoff[2];
+  uint32_t qoff[NH];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  for (int h = 0; h < NH; ++h) {
     const int r = sr + 64 * h;
     qoff[h] = r < 16 * nqb ? query_row_offset(a, b, qb0 * 16 + r) : kOOB;
   }
-  u32x4_t vq[2][kWideKC];
+  u32x4_t vq[NH][kWideKC];
   auto qload = [&](int kc) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < NH; ++h)
 #pragma unroll
       for (int t = 0; t < kWideKC; ++t) {
         const int k = (kc * kWideKC + t) * 32 + 8 * sp;
@@ -90,10 +94,13 @@ __global__ void __launch_bounds__(256) wide_sim_kernel(FwdArgs a, float* S, int 
   };
   auto qstore = [&]() {
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < NH; ++h) {
+      if (sr + 64 * h < 16 * QB) {  // rows of the block group only
 #pragma unroll
-      for (int t = 0; t < kWideKC; ++t)
-        *reinterpret_cast<u32x4_t*>(&qs[t][(sr + 64 * h) * kWideQRow + 16 * sp]) = vq[h][t];
+        for (int t = 0; t < kWideKC; ++t)
+          *reinterpret_cast<u32x4_t*>(&qs[t][(sr + 64 * h) * kWideQRow + 16 * sp]) = vq[h][t];
+      }
+    }
   };
 
   // doc rows: each lane loads token tile*16 + c, as in load_tile; rows past
@@ -128,11 +135,11 @@ __global__ void __launch_bounds__(256) wide_sim_kernel(FwdArgs a, float* S, int 
       }
   };
 
-  f32x4_t acc[kWideTW][kWideQB];
+  f32x4_t acc[kWideTW][QB];
 #pragma unroll
   for (int w = 0; w < kWideTW; ++w)
 #pragma unroll
-    for (int nb = 0; nb < kWideQB; ++nb) acc[w][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int nb = 0; nb < QB; ++nb) acc[w][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   const int nkc = (a.d + 32 * kWideKC - 1) / (32 * kWideKC);
   qload(0);
@@ -160,7 +167,7 @@ __global__ void __launch_bounds__(256) wide_sim_kernel(FwdArgs a, float* S, int 
 #pragma unroll
       for (int t = 0; t < kWideKC; ++t)
 #pragma unroll
-        for (int nb = 0; nb < kWideQB; ++nb) {
+        for (int nb = 0; nb < QB; ++nb) {
           if (nb < nqb) {  // uniform
             const u32x4_t bq = *reinterpret_cast<const u32x4_t*>(&qs[t][(16 * nb + c) * kWideQRow + 16 * g]);
 #pragma unroll
@@ -175,7 +182,7 @@ __global__ void __launch_bounds__(256) wide_sim_kernel(FwdArgs a, float* S, int 
   // result lane (c, g): doc tokens tile*16 + 4g .. +3 of query token 16*qb + c
   float* Si = S + (int64_t)il * a.Lq * ldp;
 #pragma unroll
-  for (int nb = 0; nb < kWideQB; ++nb) {
+  for (int nb = 0; nb < QB; ++nb) {
     const int q = (qb0 + nb) * 16 + c;
     if (nb < nqb && q < a.Lq) {
 #pragma unroll
@@ -240,13 +247,21 @@ hipError_t launch_kind(const FwdArgs& a, bool with_argmax, float* ws, size_t ws_
   if (chunk < 1) return hipErrorInvalidValue;
   if (chunk > items) chunk = items;
   const int ntile = (a.Ld + 15) / 16;
-  const dim3 sgrid(1u, (unsigned)((ntile + 4 * kWideTW - 1) / (4 * kWideTW)),
-                   (unsigned)(((a.Lq + 15) / 16 + kWideQB - 1) / kWideQB));
+  const int nqb = (a.Lq + 15) / 16;
+  const int qb = nqb <= 2 ? 2 : nqb <= 4 ? 4 : kWideQB;
+  const dim3 sgrid(1u, (unsigned)((ntile + 4 * kWideTW - 1) / (4 * kWideTW)), (unsigned)((nqb + qb - 1) / qb));
   for (int64_t i0 = 0; i0 < items; i0 += chunk) {
     const int n = (int)(items - i0 < chunk ? items - i0 : chunk);
-    if (ntile > 0)
-      hipLaunchKernelGGL(wide_sim_kernel<KIND>, dim3((unsigned)n, sgrid.y, sgrid.z), dim3(256), 0, s, a, ws, (int)i0,
-                         ldp);
+    if (ntile > 0) {
+      const dim3 grid((unsigned)n, sgrid.y, sgrid.z);
+      if (qb == 2) {
+        hipLaunchKernelGGL((wide_sim_kernel<KIND, 2>), grid, dim3(256), 0, s, a, ws, (int)i0, ldp);
+      } else if (qb == 4) {
+        hipLaunchKernelGGL((wide_sim_kernel<KIND, 4>), grid, dim3(256), 0, s, a, ws, (int)i0, ldp);
+      } else {
+        hipLaunchKernelGGL((wide_sim_kernel<KIND, kWideQB>), grid, dim3(256), 0, s, a, ws, (int)i0, ldp);
+      }
+    }
     if (with_argmax) {
       hipLaunchKernelGGL(wide_reduce_kernel<true>, dim3((unsigned)n), dim3(256), 0, s, a, ws, (int)i0, ldp);
     } else {
