@@ -127,6 +127,28 @@ stream_fwd_kernel(FwdArgs a) {
   // 63.6 -> 59.7 us, 200-token docs -7 %, config 4's docs -2 %; at d = 256
   // with four query blocks it lost 3.6 %).
   constexpr bool DQ = U8 && NQB >= 8;
+  // group scale loads (below): the four-tile ring, and the two-tile ring of
+  // short doc pairs when one range covers both docs' scales (JOINT)
+  constexpr bool GSM = U8 && VEC && !DQ && (P == 4 || (P == 2 && JOINT));
+  static_assert(!GSM || P == 4 || P == 2, "group scale loads map 16 lanes per tile slot");
+  static_assert(!JOINT || DOCS == 2, "a joint scale range serves two-doc group loads");
+  // uint8 DMA tiles: 16 code rows of 128 bytes (two load instructions of 8
+  // rows each), chunk j of row r at j ^ (r % 8); the scales and mins keep the
+  // group loads into registers.
+  // (uint8 queries of up to 32 tokens: config 4 62.2 -> 57.9 us, packed
+  // 64.3 -> 58.6 us; 33-64-token queries lost 5-10 % and keep the VGPR ring).
+  // U8RING = false keeps the VGPR ring for smaller uint8 workloads, and
+  // NT = false takes the default cache policy for smaller fp16/bf16 doc sets
+  // (the launch's choices, kLlcBytes).
+  constexpr bool DMA = DMA_FP || (U8RING && U8 && NQB <= 2 && KS == 4 && !KMASK && !ARGMAX && PD == 0 && GSM);
+  constexpr int RB = U8 ? 128 : 256;       // bytes of a tile row
+  constexpr int TB = 16 * RB;              // bytes of a tile
+  constexpr int TI = TB / 1024;            // DMA instructions per tile
+  constexpr int CPR = RB / 16;             // 16-byte chunks per row
+  // vector-memory instructions between two tiles' DMA loads in the steady
+  // state besides the tiles': a group's scale and min loads
+  constexpr int GL = GSM ? ((JOINT || DOCS == 1) ? 2 : 4) : 0;
+  __shared__ __attribute__((aligned(16))) unsigned char dring[DMA ? NW * P * TB : 16];
   __shared__ float red_m[DOCS][NW][QROWS];
   __shared__ int red_i[ARGMAX ? NW : 1][QROWS];
 
@@ -196,8 +218,22 @@ stream_fwd_kernel(FwdArgs a) {
   // Each wave loads every NW-th fragment of the query tile; the fragments
   // meet in LDS once the first doc tiles are in flight (q_exchange), so the
   // workgroup issues the query loads once instead of once per wave.
+  // QALIAS (fp16 rings): the LDS ring's last slot of every wave holds the
+  // fragments during the exchange (its first tile is loaded after it), so the
+  // workgroup's LDS is the ring's and four workgroups share a CU instead of
+  // three. The uint8 ring keeps its own buffer: at four workgroups per CU its
+  // packed-layout stream ran 2 % slower (more concurrent doc streams).
   constexpr int NF = NQB * KS, FPW = (NF + NW - 1) / NW;
-  __shared__ u32x4_t qs[NF][64];
+  constexpr bool QALIAS = DMA_FP && NF * 1024 <= NW * TB;
+  __shared__ u32x4_t qs_own[QALIAS ? 1 : NF][QALIAS ? 1 : 64];
+  // fragment f's 64 lanes: in wave (f % NW)'s last ring slot, or in qs_own
+  auto qfrag = [&](int f) -> u32x4_t* {
+    if constexpr (QALIAS) {
+      return reinterpret_cast<u32x4_t*>(dring + (f % NW) * P * TB + (P - 1) * TB + (f / NW) * 1024);
+    } else {
+      return &qs_own[f][0];
+    }
+  };
   u32x4_t qv[FPW];
 #pragma unroll
   for (int j = 0; j < FPW; ++j) {
@@ -221,13 +257,13 @@ stream_fwd_kernel(FwdArgs a) {
 #pragma unroll
     for (int j = 0; j < FPW; ++j) {
       const int f = wave + NW * j;
-      if (f < NF) qs[f][lane] = qv[j];
+      if (f < NF) qfrag(f)[lane] = qv[j];
     }
     __syncthreads();
 #pragma unroll
     for (int nb = 0; nb < NQB; ++nb) {
 #pragma unroll
-      for (int t = 0; t < KS; ++t) qf[nb][t] = qs[nb * KS + t][lane];
+      for (int t = 0; t < KS; ++t) qf[nb][t] = qfrag(nb * KS + t)[lane];
       qsum[nb] = 0.f;
       if constexpr (U8 && !DQ) {
         qsum[nb] = query_row_sum<KS>(qf[nb]);
@@ -248,29 +284,7 @@ stream_fwd_kernel(FwdArgs a) {
   // Sequence position -> (doc, tile of that doc); uniform over the wave.
   // Positions past the sequence read an empty range (zeros, no memory access).
   constexpr bool FIXED = !ARGMAX;  // fixed refill pattern (below)
-  // group scale loads (below): the four-tile ring, and the two-tile ring of
-  // short doc pairs when one range covers both docs' scales (JOINT)
-  constexpr bool GSM = U8 && VEC && !DQ && (P == 4 || (P == 2 && JOINT));
-  static_assert(!GSM || P == 4 || P == 2, "group scale loads map 16 lanes per tile slot");
-  static_assert(!JOINT || DOCS == 2, "a joint scale range serves two-doc group loads");
-  // uint8 DMA tiles: 16 code rows of 128 bytes (two load instructions of 8
-  // rows each), chunk j of row r at j ^ (r % 8); the scales and mins keep the
-  // group loads into registers.
-  // (uint8 queries of up to 32 tokens: config 4 62.2 -> 57.9 us, packed
-  // 64.3 -> 58.6 us; 33-64-token queries lost 5-10 % and keep the VGPR ring).
-  // U8RING = false keeps the VGPR ring for smaller uint8 workloads, and
-  // NT = false takes the default cache policy for smaller fp16/bf16 doc sets
-  // (the launch's choices, kLlcBytes).
-  constexpr bool DMA = DMA_FP || (U8RING && U8 && NQB <= 2 && KS == 4 && !KMASK && !ARGMAX && PD == 0 && GSM);
-  constexpr int RB = U8 ? 128 : 256;       // bytes of a tile row
-  constexpr int TB = 16 * RB;              // bytes of a tile
-  constexpr int TI = TB / 1024;            // DMA instructions per tile
-  constexpr int CPR = RB / 16;             // 16-byte chunks per row
-  // vector-memory instructions between two tiles' DMA loads in the steady
-  // state besides the tiles': a group's scale and min loads
-  constexpr int GL = GSM ? ((JOINT || DOCS == 1) ? 2 : 4) : 0;
   const rsrc_t nul = make_rsrc(a.D, 0u);
-  __shared__ __attribute__((aligned(16))) unsigned char dring[DMA ? NW * P * TB : 16];
   unsigned char* const myring = dring + (DMA ? wave * P * TB : 0);
   auto seq_load = [&](Tile<KIND, KS>& T, int sq, int slot) {
     const bool past = sq >= ntiles;
@@ -481,8 +495,12 @@ stream_fwd_kernel(FwdArgs a) {
   uint32_t gsc = 0, gmc = 0, gsn = 0, gmn = 0;  // group scales / mins: current, next
   if constexpr (GSM) group_sm(0, gsc, gmc);
 #pragma unroll
-  for (int s = 0; s < P; ++s) seq_load(buf[s], wave + NW * s, s);
+  for (int s = 0; s < (QALIAS ? P - 1 : P); ++s) seq_load(buf[s], wave + NW * s, s);
   q_exchange();
+  if constexpr (QALIAS) {
+    __syncthreads();  // every wave has its fragments: the last slots take their tiles
+    seq_load(buf[P - 1], wave + NW * (P - 1), P - 1);
+  }
   if constexpr (FIXED) {
     // A fixed load pattern: every group of P tiles that has a next group
     // refills all P slots, so the compiler's wait before each tile counts the
