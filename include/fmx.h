@@ -253,6 +253,7 @@ size_t fmx_fwd_topk_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld, int64_t d
  *   dD[b, j, :] = grad[b] * sum_{q : argmax[b, q] = j} Q[q, :]
  * dQ ([Lq, d]) and dD ([B, Ld, d]) are written contiguous in `dtype`, each
  * skipped when NULL. dD is fully written (zeros where no token picked a row).
+ * Streams as fmx_bwd_batched.
  *
  * Replaces flash_maxsim/flash_maxsim.py:265-286 (_FlashMaxSimFn.backward) and
  * its kernels _maxsim_bwd_dQ_kernel (:153-168) and _maxsim_bwd_dD_kernel
@@ -283,6 +284,14 @@ size_t fmx_bwd_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld, int64_t d);
  * dQ [Nq, Lq, d] and dD [B, Ld, d] are written contiguous in `dtype`, each
  * skipped when NULL; dD rows no token picked are zeros, picked rows are the
  * fp32 sum in (qi, q) order (deterministic). dD needs Ld < 2^19 (any Nq*Lq).
+ *
+ * Streams: all work is ordered on `stream`. When both dQ and dD are asked for
+ * and dD holds 2^24 bytes or more, the dQ kernels run on a second stream of
+ * the library's (one per device, created on first use, default priority),
+ * forked from and joined back to `stream` with events, so work enqueued on
+ * `stream` after the call sees both outputs. Under stream capture everything
+ * stays on `stream`. Calls from several host threads are safe; their dQ
+ * kernels share the second stream.
  *
  * Generalises fmx_bwd (which is its Nq = 1, lengths = NULL case; reference
  * flash_maxsim/flash_maxsim.py:265-286) to the batched and variable-length

@@ -164,3 +164,52 @@ def test_train_grad_only_d(oracle_mod, B, Lq, Ld, d):
     am = saved_argmax(Qn, Dn, None)
     _, dD_ref = reference_grads(oracle_mod, Qn, Dn, am, g.numpy(), None)
     np.testing.assert_allclose(Dg.grad.double().cpu().numpy(), dD_ref, rtol=2e-3, atol=ATOL)
+
+
+@pytest.mark.parametrize("Nq, B, Lq, Ld, d", [(2, 300, 32, 256, 128), (1, 40, 64, 300, 1024)])
+def test_bwd_forked_chains_match_separate_chains(Nq, B, Lq, Ld, d):
+    """With both gradients asked for and dD of 2^24 bytes or more, fmx_bwd_batched
+    runs the dQ chain on a second stream beside the dD chain and joins it to the
+    caller's stream. Its outputs must equal, byte for byte, the chains run one at
+    a time on the caller's stream (dQ alone, then dD alone: no second stream),
+    over calls back to back with changing gradients, each result copied on the
+    caller's stream right after its call (a missing join would let the copy read
+    an unfinished dQ)."""
+    from flash_maxsim_amd import _lib
+
+    assert B * Ld * d * 2 >= 1 << 24
+    gen = torch.Generator().manual_seed(1700 + d)
+    Qk = _prep(torch.randn(Nq, Lq, d, generator=gen).to(torch.float16).to(DEV), torch.float16)
+    Dk = _prep(torch.randn(B, Ld, d, generator=gen).to(torch.float16).to(DEV), torch.float16)
+    lengths = torch.randint(1, Ld + 1, (B,), generator=gen, dtype=torch.int32)
+    lengths[3] = 0
+    lengths[5] = Ld
+    lengths = lengths.to(DEV)
+    _, am = _launch_fwd(Qk, Dk, lengths, Nq, B, Lq, Ld, d, True, True)
+    lib = _lib.load()
+    nbytes = lib.fmx_bwd_batched_workspace_bytes(Nq, B, Lq, Ld, d)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+
+    def call(g, dQ, dD):
+        rc = lib.fmx_bwd_batched(
+            _lib.dtype_code(Qk), Qk.data_ptr(), Qk.stride(0), Qk.stride(1), Dk.data_ptr(), Dk.stride(0),
+            Dk.stride(1), lengths.data_ptr(), am.data_ptr(), g.data_ptr(), g.stride(0), g.stride(1),
+            _lib.ptr(dQ), _lib.ptr(dD), Nq, B, Lq, Ld, d, ws.data_ptr(), nbytes,
+            torch.cuda.current_stream().cuda_stream,
+        )
+        _lib.check(rc)
+
+    forked = []
+    for it in range(4):
+        g = torch.randn(Nq, B, generator=gen).to(DEV)
+        dQ = torch.empty(Nq, Lq, d, dtype=torch.float16, device=DEV)
+        dD = torch.empty(B, Ld, d, dtype=torch.float16, device=DEV)
+        call(g, dQ, dD)
+        forked.append((g, dQ.clone(), dD.clone()))
+    for g, fQ, fD in forked:
+        sQ = torch.empty(Nq, Lq, d, dtype=torch.float16, device=DEV)
+        sD = torch.empty(B, Ld, d, dtype=torch.float16, device=DEV)
+        call(g, sQ, None)
+        call(g, None, sD)
+        assert torch.count_nonzero(sQ) > 0 and torch.count_nonzero(sD) > 0
+        assert torch.equal(fQ, sQ) and torch.equal(fD, sD)
