@@ -173,9 +173,9 @@ __global__ void __launch_bounds__(256) bwd_dq_finalize_kernel(BwdArgs a) {
 
 constexpr int kEntryBits = 13;  // entries of one chunk < 2^13 (kDdChunk)
 constexpr uint32_t kNoRow = 0xffffffffu;
-constexpr int kDdMaxPasses = 4;
+constexpr int kDdMaxPasses = 4;  // workgroup row passes per dD writer slab, at most
 // dD sizes from which the dQ chain runs on a second stream (launch_bwd_t).
-constexpr int64_t kBwdForkBytes = (int64_t)1 << 24;  // workgroup row passes per dD writer slab, at most
+constexpr int64_t kBwdForkBytes = (int64_t)1 << 24;
 
 // dD index, one workgroup per (doc, chunk of kDdChunk consecutive (query,
 // token) entries). The chunk's entries e become keys row << 13 | (e - e0) in

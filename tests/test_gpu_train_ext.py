@@ -213,3 +213,60 @@ def test_bwd_forked_chains_match_separate_chains(Nq, B, Lq, Ld, d):
         call(g, None, sD)
         assert torch.count_nonzero(sQ) > 0 and torch.count_nonzero(sD) > 0
         assert torch.equal(fQ, sQ) and torch.equal(fD, sD)
+
+
+@pytest.mark.parametrize(
+    "Nq, B, Lq, Ld, d",
+    [(1, 9, 100, 7, 300), (3, 5, 100, 6, 1100), (4, 4, 128, 5, 520), (1, 3, 513, 9, 264), (2, 6, 40, 3, 128)],
+)
+def test_bwd_exact_on_integer_grid(Nq, B, Lq, Ld, d):
+    """fmx_bwd_batched on a given argmax with many entries per doc row (Ld of 3-9
+    rows, up to 513 (query, token) entries per doc), integer Q, D and gradients:
+    every fp32 sum is exact, so dD and dQ must equal integer arithmetic, whatever
+    the order of the sums. d % 8 != 0 (partial chunks), d > 1024 (rows wider than
+    a wave's 64 lanes of 8 elements), several queries, empty docs and ragged
+    lengths."""
+    from flash_maxsim_amd import _lib
+
+    gen = torch.Generator().manual_seed(1800 + d + Lq)
+    Q = torch.randint(-1, 2, (Nq, Lq, d), generator=gen)
+    D = torch.randint(-2, 3, (B, Ld, d), generator=gen)
+    g = torch.tensor([-1, 1, 2])[torch.randint(0, 3, (Nq, B), generator=gen)]
+    lengths = torch.randint(1, Ld + 1, (B,), generator=gen, dtype=torch.int32)
+    lengths[1] = 0
+    am = torch.minimum(
+        torch.randint(0, Ld, (Nq, B, Lq), generator=gen, dtype=torch.int32),
+        (lengths.clamp(min=1) - 1)[None, :, None],
+    )
+    dD_ref = torch.zeros(B, Ld, d, dtype=torch.int64)
+    dQ_ref = torch.zeros(Nq, Lq, d, dtype=torch.int64)
+    for qi in range(Nq):
+        for b in range(B):
+            if lengths[b] <= 0:
+                continue
+            dD_ref[b].index_add_(0, am[qi, b].long(), g[qi, b] * Q[qi])
+            dQ_ref[qi] += g[qi, b] * D[b, am[qi, b].long()]
+    assert dD_ref.abs().max() <= 2048 and dQ_ref.abs().max() <= 2048
+
+    dp = (d + 7) // 8 * 8  # the C-ABI takes rows padded to a multiple of 8 elements
+    Qd = torch.zeros(Nq, Lq, dp, dtype=torch.float16)
+    Qd[..., :d] = Q.to(torch.float16)
+    Dd = torch.zeros(B, Ld, dp, dtype=torch.float16)
+    Dd[..., :d] = D.to(torch.float16)
+    Qd, Dd = Qd.to(DEV), Dd.to(DEV)
+    gd = g.to(torch.float32).to(DEV)
+    amd = am.reshape(Nq * B, Lq).contiguous().to(DEV)
+    ld = lengths.to(DEV)
+    dQ = torch.full((Nq, Lq, d), float("nan"), dtype=torch.float16, device=DEV)
+    dD = torch.full((B, Ld, d), float("nan"), dtype=torch.float16, device=DEV)
+    lib = _lib.load()
+    nbytes = lib.fmx_bwd_batched_workspace_bytes(Nq, B, Lq, Ld, d)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    rc = lib.fmx_bwd_batched(
+        _lib.FMX_DTYPE_F16, Qd.data_ptr(), Qd.stride(0), Qd.stride(1), Dd.data_ptr(), Dd.stride(0), Dd.stride(1),
+        ld.data_ptr(), amd.data_ptr(), gd.data_ptr(), gd.stride(0), gd.stride(1), dQ.data_ptr(), dD.data_ptr(),
+        Nq, B, Lq, Ld, d, ws.data_ptr(), nbytes, torch.cuda.current_stream().cuda_stream,
+    )
+    _lib.check(rc)
+    assert torch.equal(dD.cpu().to(torch.int64), dD_ref)
+    assert torch.equal(dQ.cpu().to(torch.int64), dQ_ref)
