@@ -8,8 +8,10 @@
  *
  * Conventions (all entry points):
  *  - Every tensor pointer is a device pointer owned by the caller. The library
- *    allocates nothing; scratch space is a caller-provided workspace whose size
- *    the matching *_workspace_bytes() function returns (0 means none needed).
+ *    allocates no device memory; scratch space is a caller-provided workspace
+ *    whose size the matching *_workspace_bytes() function returns (0 means none
+ *    needed). The backward creates one stream and two events per device on
+ *    first use (see fmx_bwd_batched).
  *  - Strides are in elements of the tensor's type. The innermost (d) stride is
  *    1. Row strides of Q and D must be multiples of 8 elements, doc strides of
  *    D multiples of 8, and Q, D 16-byte aligned; d itself may be anything
