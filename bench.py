@@ -23,6 +23,7 @@ Configs (the driver's line is the default, c1):
              Q[100,32,128] x D[100,50,300,128]
   c4         config 4, uint8 docs [5000,1024,128], lengths U[32,1024]
   c4_packed  config 4's docs in the packed layout
+  c4_packed_sorted  the same, docs laid out longest first (sort_by_length)
   c4_lq128   config 4's docs against a 128-token query
   mid        the reference's published "medium" row: Q[128,128] x D[1000,1024,128]
   c5         config 5, training forward + backward, Q[128,1024] x D[1000,512,1024]
@@ -122,7 +123,8 @@ def _realign(packed, align: int):
     scales = torch.zeros(T, dtype=packed.scales.dtype, device=L.device)
     mins = torch.zeros(T, dtype=packed.mins.dtype, device=L.device)
     codes[dst], scales[dst], mins[dst] = packed.codes[src], packed.scales[src], packed.mins[src]
-    return fm.PackedInt8Docs(codes, scales, mins, (start // 4).contiguous(), packed.lengths, packed.max_len)
+    return fm.PackedInt8Docs(codes, scales, mins, (start // 4).contiguous(), packed.lengths, packed.max_len,
+                             packed.doc_ids)
 
 
 def build(name: str, rotate: int, doc_align: int = 4) -> Workload:
@@ -246,7 +248,7 @@ def build(name: str, rotate: int, doc_align: int = 4) -> Workload:
         return Workload(cfg, steps, Nq * B, "pairs/s", roof, cpu, Nq * B,
                         f"maxsim_naive fp32, per-query loop over all {Nq} x {B} pairs")
 
-    if name in ("c4", "c4_packed", "c4_lq128"):
+    if name in ("c4", "c4_packed", "c4_packed_sorted", "c4_lq128"):
         B, Ld, d = 5000, 1024, 128
         Lq = 128 if name == "c4_lq128" else 32
         Q = sim((Lq, d), 41 if Lq == 32 else 45, f16)
@@ -265,24 +267,26 @@ def build(name: str, rotate: int, doc_align: int = 4) -> Workload:
         Qc = Q.float()
         cpu = lambda: fm.maxsim_naive(Qc, fm.dequantize_int8(cc, cs, cm), cl)  # noqa: E731
         sample = f"maxsim_naive fp32 against dequantize_int8 of the first {n} docs, with their lengths"
-        if name == "c4_packed":
+        if name in ("c4_packed", "c4_packed_sorted"):
+            srt = name == "c4_packed_sorted"
             Dg = torch.empty(B, Ld, d, dtype=torch.float32, device=dev)
             for b0 in range(0, B, 500):
                 Dg[b0:b0 + 500] = sim((500, Ld, d), 42 + b0, torch.float32, dev)
-            packed = fm.quantize_int8_packed(Dg, lengths)
+            packed = fm.quantize_int8_packed(Dg, lengths, sort_by_length=srt)
             del Dg, codes, scales, mins
             if doc_align > 4:
                 packed = _realign(packed, doc_align)
             packs = [packed] + [fm.PackedInt8Docs(packed.codes.clone(), packed.scales.clone(), packed.mins.clone(),
-                                                  packed.tok_group, packed.lengths, packed.max_len)
+                                                  packed.tok_group, packed.lengths, packed.max_len, packed.doc_ids)
                                 for _ in range(max(1, rotate) - 1)]
             cfg = {"workload": f"int8 packed varlen flash_maxsim_int8_packed Q[{Lq},{d}] x {B} docs of "
-                               f"U[32,1024] tokens, d={d} u8 ({packed.codes.shape[0]} packed rows)", "B": B,
+                               f"U[32,1024] tokens, d={d} u8 ({packed.codes.shape[0]} packed rows"
+                               f"{', longest first' if srt else ''})", "B": B,
                    "Lq": Lq, "d": d, "sum_len": tot}
             if doc_align > 4:
                 cfg["doc_align_rows"] = doc_align
             steps = [lambda p=p: fm.flash_maxsim_int8_packed(Qd, p) for p in packs]
-            algo = tot * (d + 4) + Lq * d * 2 + B * 16  # + tok_group, lengths, scores
+            algo = tot * (d + 4) + Lq * d * 2 + B * (20 if srt else 16)  # + tok_group, lengths, scores (, doc_ids)
         else:
             sets = [(codes, scales, mins)] + [(codes.clone(), scales.clone(), mins.clone())
                                               for _ in range(max(1, rotate) - 1)]

@@ -56,12 +56,12 @@ _SIGNATURES = {
     ),
     "fmx_fwd_packed": (
         _int,
-        [_int, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _ptr, _i64, _i64, _i64, _ptr, _size, _ptr],
+        [_int, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _ptr, _size, _ptr],
     ),
     "fmx_fwd_packed_workspace_bytes": (_size, [_i64, _i64, _i64, _i64]),
     "fmx_fwd_int8_packed": (
         _int,
-        [_ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr, _i64, _ptr, _ptr, _ptr, _i64, _i64, _i64, _ptr, _size, _ptr],
+        [_ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr, _i64, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _ptr, _size, _ptr],
     ),
     "fmx_fwd_int8_packed_workspace_bytes": (_size, [_i64, _i64, _i64, _i64]),
     "fmx_topk": (_int, [_ptr, _i64, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, _size, _ptr]),

@@ -171,7 +171,7 @@ int fwd_impl(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, c
              int64_t d_stride_l, const int64_t* tok_group, int64_t tok_rows, const int32_t* lengths, float* scores,
              int64_t s_stride_n, int64_t s_stride_b, int32_t* argmax, int64_t Nq, int64_t B, int64_t Lq, int64_t Ld,
              int64_t d, int shared_docs, void* workspace, size_t workspace_bytes, void* stream,
-             bool noalloc = false) {
+             bool noalloc = false, const int32_t* doc_ids = nullptr) {
   if (dtype != FMX_DTYPE_F16 && dtype != FMX_DTYPE_BF16) return fail(FMX_ERR_INVALID, "unknown dtype %d", dtype);
   int rc = check_common(Nq, B, Lq, Ld, d, q_stride_l, d_stride_b, d_stride_l, 2);
   if (rc) return rc;
@@ -216,6 +216,7 @@ int fwd_impl(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, c
   a.partial = static_cast<float*>(workspace);
   a.tok_group = tok_group;
   a.tok_rows = tok_rows;
+  a.doc_ids = doc_ids;
   a.sq_n = Nq > 1 ? q_stride_n : 0;
   a.sq_l = q_stride_l;
   a.sd_b = d_stride_b;
@@ -248,7 +249,7 @@ int fwd_impl(int dtype, const void* Q, int64_t q_stride_n, int64_t q_stride_l, c
 int int8_impl(const void* Q, int64_t q_stride_l, const uint8_t* D, int64_t d_stride_b, int64_t d_stride_l,
               const void* scales, const void* mins, int64_t sm_stride_b, const int64_t* tok_group, int64_t tok_rows,
               const int32_t* lengths, float* scores, int64_t B, int64_t Lq, int64_t Ld, int64_t d, void* workspace,
-              size_t workspace_bytes, void* stream) {
+              size_t workspace_bytes, void* stream, const int32_t* doc_ids = nullptr) {
   int rc = check_common(1, B, Lq, Ld, d, q_stride_l, d_stride_b, d_stride_l, 1);
   if (rc) return rc;
   if (B == 0) return ok();
@@ -282,6 +283,7 @@ int int8_impl(const void* Q, int64_t q_stride_l, const uint8_t* D, int64_t d_str
   a.partial = static_cast<float*>(workspace);
   a.tok_group = tok_group;
   a.tok_rows = tok_rows;
+  a.doc_ids = doc_ids;
   a.sq_n = 0;
   a.sq_l = q_stride_l;
   a.sd_b = d_stride_b;
@@ -396,14 +398,15 @@ size_t fmx_fwd_packed_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld_max, int
 }
 
 int fmx_fwd_packed(int dtype, const void* Q, int64_t q_stride_l, int64_t Lq, const void* D, int64_t d_stride_l,
-                   int64_t tok_rows, const int64_t* tok_group, const int32_t* lengths, float* scores, int64_t B,
-                   int64_t Ld_max, int64_t d, void* workspace, size_t workspace_bytes, void* stream) {
+                   int64_t tok_rows, const int64_t* tok_group, const int32_t* lengths, const int32_t* doc_ids,
+                   float* scores, int64_t B, int64_t Ld_max, int64_t d, void* workspace, size_t workspace_bytes,
+                   void* stream) {
   if (B > 0) {
     const int rc = check_packed(tok_group, lengths, tok_rows);
     if (rc) return rc;
   }
   return fwd_impl(dtype, Q, 0, q_stride_l, D, 0, d_stride_l, tok_group, tok_rows, lengths, scores, 0, 1, nullptr,
-                  1, B, Lq, Ld_max, d, 1, workspace, workspace_bytes, stream);
+                  1, B, Lq, Ld_max, d, 1, workspace, workspace_bytes, stream, false, doc_ids);
 }
 
 size_t fmx_fwd_int8_packed_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld_max, int64_t d) {
@@ -412,14 +415,14 @@ size_t fmx_fwd_int8_packed_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld_max
 
 int fmx_fwd_int8_packed(const void* Q, int64_t q_stride_l, int64_t Lq, const uint8_t* codes, int64_t c_stride_l,
                         const void* scales, const void* mins, int64_t tok_rows, const int64_t* tok_group,
-                        const int32_t* lengths, float* scores, int64_t B, int64_t Ld_max, int64_t d,
-                        void* workspace, size_t workspace_bytes, void* stream) {
+                        const int32_t* lengths, const int32_t* doc_ids, float* scores, int64_t B, int64_t Ld_max,
+                        int64_t d, void* workspace, size_t workspace_bytes, void* stream) {
   if (B > 0) {
     const int rc = check_packed(tok_group, lengths, tok_rows);
     if (rc) return rc;
   }
   return int8_impl(Q, q_stride_l, codes, 0, c_stride_l, scales, mins, 0, tok_group, tok_rows, lengths, scores, B,
-                   Lq, Ld_max, d, workspace, workspace_bytes, stream);
+                   Lq, Ld_max, d, workspace, workspace_bytes, stream, doc_ids);
 }
 
 int fmx_quantize_int8(int src_dtype, const void* src, int64_t s_stride_b, int64_t s_stride_l, int64_t B, int64_t Ld,

@@ -292,7 +292,7 @@ __global__ void __launch_bounds__(512) splitd_fwd_kernel(FwdArgs a) {
     const float total = wave_sum(partsum);
     if (lane == 0) {
       if (npass == 1) {
-        a.scores[(int64_t)qi * a.ss_n + (int64_t)b * a.ss_b] = total;
+        store_score(a, qi, b, total);
       } else {
         a.partial[(int64_t)pass * a.Nq * a.B + item] = total;
       }
@@ -312,7 +312,7 @@ __global__ void __launch_bounds__(256) splitd_sum_passes_kernel(FwdArgs a, int n
   float s = 0.f;
   for (int p = 0; p < npass; ++p) s += a.partial[(int64_t)p * items + item];
   const int64_t qi = item / a.B, b = item - qi * a.B;
-  a.scores[qi * a.ss_n + b * a.ss_b] = s;
+  store_score(a, qi, b, s);
 }
 
 template <int KIND, int NQB, int KSW, bool KMASK, bool ARGMAX, bool VEC = true, bool C16 = VEC>

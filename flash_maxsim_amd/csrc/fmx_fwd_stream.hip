@@ -591,7 +591,7 @@ stream_fwd_kernel(FwdArgs a) {
     const float total = wave_sum(part);
     if (lane == 0) {
       if (npass == 1) {
-        a.scores[(int64_t)qi * a.ss_n + (int64_t)(b + dd) * a.ss_b] = total;
+        store_score(a, qi, b + dd, total);
       } else {
         a.partial[(int64_t)pass * a.Nq * a.B + item] = total;
       }
@@ -607,7 +607,7 @@ __global__ void __launch_bounds__(256) sum_passes_kernel(FwdArgs a, int npass) {
   float s = 0.f;
   for (int p = 0; p < npass; ++p) s += a.partial[(int64_t)p * items + item];
   const int64_t qi = item / a.B, b = item - qi * a.B;
-  a.scores[qi * a.ss_n + b * a.ss_b] = s;
+  store_score(a, qi, b, s);
 }
 
 
@@ -754,7 +754,7 @@ __global__ void __launch_bounds__(256) stream_u8_shared_kernel(FwdArgs a) {
     float total = part[0];
 #pragma unroll
     for (int w = 1; w < kStreamWaves; ++w) total += part[w];
-    a.scores[(int64_t)b * a.ss_b] = total;
+    store_score(a, 0, b, total);
   }
 }
 

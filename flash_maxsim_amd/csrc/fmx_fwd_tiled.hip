@@ -473,7 +473,7 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
           const float sum = group_sum(in ? v : 0.f, lq);
           if (in && (lane & (lq - 1)) == 0) {
             const int64_t qi = (row0 + r) >> lsh;
-            a.scores[qi * a.ss_n + (int64_t)b * a.ss_b] = sum;
+            store_score(a, qi, b, sum);
           }
         }
         par ^= 1;
@@ -492,7 +492,7 @@ tiled_fwd_kernel(FwdArgs a, int nRB, int G, int xcd_map) {
       if (lane == 0) {
         const bool whole = ra == qi * a.Lq && rz == (qi + 1) * a.Lq;
         if (whole) {
-          a.scores[qi * a.ss_n + (int64_t)b * a.ss_b] = sum;
+          store_score(a, qi, b, sum);
         } else {
           a.partial[(int64_t)rb * a.Nq * a.B + qi * a.B + b] = sum;
         }
@@ -701,7 +701,7 @@ __global__ void __launch_bounds__(256) tiled_sum_parts_kernel(FwdArgs a, int R) 
   if (rb0 == rb1) return;  // written directly by its row block
   float s = 0.f;
   for (int64_t rb = rb0; rb <= rb1; ++rb) s += a.partial[rb * items + item];
-  a.scores[qi * a.ss_n + b * a.ss_b] = s;
+  store_score(a, qi, b, s);
 }
 
 template <int KIND, int NW, int NB, int KS, bool KMASK, bool ARGMAX>

@@ -233,7 +233,7 @@ __global__ void __launch_bounds__(256) wide_reduce_kernel(FwdArgs a, const float
   }
   if (lane == 0) part[wave] = sum;
   __syncthreads();
-  if (threadIdx.x == 0) a.scores[(int64_t)qi * a.ss_n + (int64_t)b * a.ss_b] = ((part[0] + part[1]) + part[2]) + part[3];
+  if (threadIdx.x == 0) store_score(a, qi, b, ((part[0] + part[1]) + part[2]) + part[3]);
 }
 
 int wide_ldp(int Ld) { return (Ld + 15) & ~15; }

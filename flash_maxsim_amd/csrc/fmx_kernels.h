@@ -30,6 +30,9 @@ struct FwdArgs {
   const int64_t* tok_group;   // packed docs: doc row r starts at token row 4*tok_group[r]
                               // (then sd_b and sm_b are unused), or null
   int64_t tok_rows;           // packed docs: token rows in D (reads are clamped to them)
+  const int32_t* doc_ids;     // packed docs laid out in another order than numbered: the
+                              // score column of doc row b is doc_ids[b] (ids outside [0, B)
+                              // are not written), or null (= b)
   int shared_docs;            // doc row of (query qi, doc b) is b, else qi*B + b
   int vec;                    // uint8 docs, bit 0: 16-byte aligned code rows and scales/mins
                               // readable 4 tokens per 8-byte load; bit 1: 16-byte aligned

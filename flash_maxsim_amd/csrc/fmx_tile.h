@@ -69,6 +69,19 @@ __device__ __forceinline__ int64_t tok_group_of(const FwdArgs& a, int64_t drow) 
                    (uint32_t)__builtin_amdgcn_readfirstlane((int)v));
 }
 
+// scores[qi, column of doc b]: b itself, or doc_ids[b] for packed docs laid
+// out in another order than they are numbered (an id outside [0, B) is not
+// written).
+__device__ __forceinline__ void store_score(const FwdArgs& a, int64_t qi, int64_t b, float v) {
+  int64_t col = b;
+  if (a.doc_ids) {
+    const int32_t id = a.doc_ids[b];
+    if ((uint32_t)id >= (uint32_t)a.B) return;
+    col = id;
+  }
+  a.scores[qi * a.ss_n + col * a.ss_b] = v;
+}
+
 // First element of doc row `drow` of the document operand: drow * sd_b, or
 // for packed docs the start of its token group, 4 * tok_group[drow] rows in.
 // UNIFORM reads tok_group through tok_group_of (the doc resources below); the

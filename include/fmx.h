@@ -196,21 +196,31 @@ int fmx_quantize_int8(int src_dtype, const void* src, int64_t s_stride_b, int64_
  * [0, Ld_max]) are required; reads are clamped to the T = tok_rows rows of D.
  * Scores equal fmx_fwd / fmx_fwd_int8 (Nq = 1) on the padded equivalent.
  *
+ * doc_ids (int32 [B], may be NULL): the docs may be laid out in another order
+ * than they are numbered. Entry b of tok_group and lengths then describes the
+ * b-th doc in that order (its slot) and doc_ids[b] is the doc's number: its
+ * score goes to scores[doc_ids[b]]. doc_ids must be a permutation of 0..B-1;
+ * an entry outside [0, B) is skipped (that score is not written). NULL: slot b
+ * is doc b. Laying docs out longest first and passing that order here scans
+ * variable-length docs faster (concurrent workgroups then stream docs of
+ * similar length side by side).
+ *
  *   Q        [Lq, d]   dtype (fp16 for int8), row stride q_stride_l
  *   D/codes  [T, d]    dtype / uint8, row stride d_stride_l / c_stride_l
  *   scales   [T]       fp16 (int8 only); mins likewise
  *   scores   [B]       fp32, contiguous
  */
 int fmx_fwd_packed(int dtype, const void* Q, int64_t q_stride_l, int64_t Lq, const void* D, int64_t d_stride_l,
-                   int64_t tok_rows, const int64_t* tok_group, const int32_t* lengths, float* scores, int64_t B,
-                   int64_t Ld_max, int64_t d, void* workspace, size_t workspace_bytes, void* stream);
+                   int64_t tok_rows, const int64_t* tok_group, const int32_t* lengths, const int32_t* doc_ids,
+                   float* scores, int64_t B, int64_t Ld_max, int64_t d, void* workspace, size_t workspace_bytes,
+                   void* stream);
 
 size_t fmx_fwd_packed_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld_max, int64_t d);
 
 int fmx_fwd_int8_packed(const void* Q, int64_t q_stride_l, int64_t Lq, const uint8_t* codes, int64_t c_stride_l,
                         const void* scales, const void* mins, int64_t tok_rows, const int64_t* tok_group,
-                        const int32_t* lengths, float* scores, int64_t B, int64_t Ld_max, int64_t d,
-                        void* workspace, size_t workspace_bytes, void* stream);
+                        const int32_t* lengths, const int32_t* doc_ids, float* scores, int64_t B, int64_t Ld_max,
+                        int64_t d, void* workspace, size_t workspace_bytes, void* stream);
 
 size_t fmx_fwd_int8_packed_workspace_bytes(int64_t B, int64_t Lq, int64_t Ld_max, int64_t d);
 

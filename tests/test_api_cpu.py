@@ -172,9 +172,9 @@ def test_quantize_and_packed_reject_bad_arguments(lib):
     rc = lib.fmx_quantize_int8(2, FAKE, 300 * 128, 128, 10, 300, 128, FAKE, FAKE, -1, FAKE, 128, FAKE, FAKE, 0, None)
     assert rc == FMX_ERR_INVALID and "tok_rows" in lib.fmx_last_error().decode()
     assert lib.fmx_quantize_int8(2, None, 0, 128, 0, 300, 128, None, None, 0, None, 128, None, None, 300, None) == FMX_OK
-    rc = lib.fmx_fwd_packed(0, FAKE, 128, 32, FAKE, 128, 1000, None, FAKE, FAKE, 10, 300, 128, None, 0, None)
+    rc = lib.fmx_fwd_packed(0, FAKE, 128, 32, FAKE, 128, 1000, None, FAKE, None, FAKE, 10, 300, 128, None, 0, None)
     assert rc == FMX_ERR_INVALID and "tok_group" in lib.fmx_last_error().decode()
-    rc = lib.fmx_fwd_int8_packed(FAKE, 128, 32, FAKE, 128, FAKE, FAKE, 1000, FAKE, None, FAKE, 10, 300, 128,
+    rc = lib.fmx_fwd_int8_packed(FAKE, 128, 32, FAKE, 128, FAKE, FAKE, 1000, FAKE, None, None, FAKE, 10, 300, 128,
                                  None, 0, None)
     assert rc == FMX_ERR_INVALID and "lengths" in lib.fmx_last_error().decode()
     assert lib.fmx_fwd_packed_workspace_bytes(10, 32, 300, 128) == 0
@@ -316,3 +316,28 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libflashmaxsim.so")
     with pytest.raises(RuntimeError, match="missing"):
         _lib.load()
+
+
+def test_pack_docs_sorted_layout_cpu():
+    """pack_docs(sort_by_length=True) on the CPU: slots longest first (stable
+    among equal lengths), tok_group and lengths per slot, slot s holding the
+    rows of doc doc_ids[s] back to back in 4-row groups, zero rows between."""
+    import flash_maxsim_amd as fm
+
+    B, Ld, d = 9, 11, 5
+    D = torch.arange(B * Ld * d, dtype=torch.float32).reshape(B, Ld, d).half()
+    lengths = torch.tensor([3, 11, 0, 7, 7, 1, 11, 4, 2], dtype=torch.int32)
+    p = fm.pack_docs(D, lengths, sort_by_length=True)
+    ids = p.doc_ids.long()
+    assert p.doc_ids.dtype == torch.int32
+    assert ids.tolist() == [1, 6, 3, 4, 7, 0, 8, 5, 2]
+    assert p.lengths.tolist() == [11, 11, 7, 7, 4, 3, 2, 1, 0]
+    groups = (p.lengths.long() + 3) // 4
+    assert p.tok_group.tolist() == (torch.cumsum(groups, 0) - groups).tolist()
+    assert p.tokens.shape[0] == 4 * int(groups.sum()) and p.max_len == 11
+    for s in range(B):
+        r0, n = 4 * int(p.tok_group[s]), int(p.lengths[s])
+        assert torch.equal(p.tokens[r0:r0 + n], D[ids[s], :n])
+        assert torch.all(p.tokens[r0 + n:r0 + 4 * int(groups[s])] == 0)
+    plain = fm.pack_docs(D, lengths)
+    assert plain.doc_ids is None and plain.lengths.tolist() == lengths.tolist()

@@ -270,3 +270,72 @@ def test_quantize_packed_respects_tok_rows(oracle_mod):
         r0 = 4 * int(tg[b])
         n = max(0, min(Ld, T - r0))
         np.testing.assert_array_equal(got[r0:r0 + n], c_ref[b, :n])
+
+
+@pytest.mark.parametrize(
+    "kind, Lq, Ld, d",
+    [("f16", 32, 90, 128), ("f16", 32, 40, 128), ("f16", 300, 80, 128), ("f16", 100, 80, 128),
+     ("f16", 32, 80, 1024), ("f16", 8, 20, 4100), ("u8", 32, 90, 128), ("u8", 200, 90, 128),
+     ("u8", 100, 77, 128), ("u8", 16, 90, 512)],
+)
+def test_packed_sorted_by_length_same_scores(kind, Lq, Ld, d):
+    """Docs laid out longest first (sort_by_length): every kernel route writes
+    slot s's score to doc doc_ids[s], so the scores equal the unsorted layout's
+    bit for bit (the same rows through the same arithmetic)."""
+    B = 300
+    gen = torch.Generator().manual_seed(1900 + Lq + d)
+    Q = sim((Lq, d), 1901 + d)
+    x = sim((B, Ld, d), 1902 + Lq, torch.float32 if kind == "u8" else torch.float16)
+    lengths = torch.randint(0, Ld + 1, (B,), generator=gen, dtype=torch.int32)
+    lengths[:4] = torch.tensor([0, Ld, 1, 0], dtype=torch.int32)
+    if kind == "u8":
+        plain = fm.quantize_int8_packed(x.to(DEV), lengths.to(DEV))
+        srt = fm.quantize_int8_packed(x.to(DEV), lengths.to(DEV), sort_by_length=True)
+        want = fm.flash_maxsim_int8_packed(Q.to(DEV), plain)
+        got = fm.flash_maxsim_int8_packed(Q.to(DEV), srt)
+        rows_plain, rows_srt = plain.codes, srt.codes
+    else:
+        plain = fm.pack_docs(x.to(DEV), lengths.to(DEV))
+        srt = fm.pack_docs(x.to(DEV), lengths.to(DEV), sort_by_length=True)
+        want = fm.flash_maxsim_packed(Q.to(DEV), plain)
+        got = fm.flash_maxsim_packed(Q.to(DEV), srt)
+        rows_plain, rows_srt = plain.tokens, srt.tokens
+    assert plain.doc_ids is None and srt.doc_ids is not None
+    ids = srt.doc_ids.long().cpu()
+    assert torch.equal(torch.sort(ids).values, torch.arange(B))
+    assert torch.all(srt.lengths[:-1] >= srt.lengths[1:])
+    assert torch.equal(srt.lengths.cpu(), lengths[ids])
+    for s in (0, 1, B // 2, B - 1):  # slot s holds doc ids[s]'s rows
+        b, n = int(ids[s]), int(lengths[ids[s]])
+        a0, p0 = 4 * int(srt.tok_group[s]), 4 * int(plain.tok_group[b])
+        assert torch.equal(rows_srt[a0:a0 + n], rows_plain[p0:p0 + n])
+    np.testing.assert_array_equal(got.cpu().numpy(), want.cpu().numpy())
+
+
+def test_packed_doc_ids_out_of_range_not_written():
+    """fmx_fwd_packed with doc_ids holding ids outside [0, B): those slots'
+    scores are not written (the columns of the docs they displaced keep what
+    the caller put there), every other doc's score lands in its column."""
+    from flash_maxsim_amd import _lib
+
+    B, Ld, d, Lq = 64, 50, 128, 32
+    Q = sim((Lq, d), 1910).to(DEV)
+    D = sim((B, Ld, d), 1911).to(DEV)
+    lengths = torch.randint(1, Ld + 1, (B,), generator=torch.Generator().manual_seed(1912), dtype=torch.int32)
+    packed = fm.pack_docs(D, lengths.to(DEV), sort_by_length=True)
+    want = fm.flash_maxsim_packed(Q, packed)
+    ids = packed.doc_ids.clone()
+    lost = [int(ids[3]), int(ids[40])]
+    ids[3], ids[40] = B, -7
+    scores = torch.full((B,), 7.0, dtype=torch.float32, device=DEV)
+    lib = _lib.load()
+    rc = lib.fmx_fwd_packed(
+        _lib.dtype_code(Q), Q.data_ptr(), Q.stride(0), Lq, packed.tokens.data_ptr(), packed.tokens.stride(0),
+        packed.tokens.shape[0], packed.tok_group.data_ptr(), packed.lengths.data_ptr(), ids.data_ptr(),
+        scores.data_ptr(), B, packed.max_len, d, None, 0, torch.cuda.current_stream().cuda_stream,
+    )
+    _lib.check(rc)
+    keep = torch.ones(B, dtype=torch.bool)
+    keep[lost] = False
+    assert torch.all(scores.cpu()[~keep] == 7.0)
+    assert torch.equal(scores.cpu()[keep], want.cpu()[keep])
