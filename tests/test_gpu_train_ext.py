@@ -270,3 +270,54 @@ def test_bwd_exact_on_integer_grid(Nq, B, Lq, Ld, d):
     _lib.check(rc)
     assert torch.equal(dD.cpu().to(torch.int64), dD_ref)
     assert torch.equal(dQ.cpu().to(torch.int64), dQ_ref)
+
+
+def test_bwd_graph_capture_replays():
+    """fmx_bwd_batched captured into a HIP graph at a size that forks the dQ
+    chain when run eagerly: under capture both chains stay on the capturing
+    stream. Every replay, with eager work and synchronisations between them,
+    must equal the eager result byte for byte."""
+    from flash_maxsim_amd import _lib
+
+    Nq, B, Lq, Ld, d = 1, 300, 32, 256, 128
+    assert B * Ld * d * 2 >= 1 << 24
+    gen = torch.Generator().manual_seed(2000)
+    Qk = _prep(torch.randn(Nq, Lq, d, generator=gen).to(torch.float16).to(DEV), torch.float16)
+    Dk = _prep(torch.randn(B, Ld, d, generator=gen).to(torch.float16).to(DEV), torch.float16)
+    lengths = torch.randint(1, Ld + 1, (B,), generator=gen, dtype=torch.int32).to(DEV)
+    _, am = _launch_fwd(Qk, Dk, lengths, Nq, B, Lq, Ld, d, True, True)
+    g = torch.randn(Nq, B, generator=gen).to(DEV)
+    lib = _lib.load()
+    nbytes = lib.fmx_bwd_batched_workspace_bytes(Nq, B, Lq, Ld, d)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    dQ = torch.empty(Nq, Lq, d, dtype=torch.float16, device=DEV)
+    dD = torch.empty(B, Ld, d, dtype=torch.float16, device=DEV)
+
+    def call():
+        rc = lib.fmx_bwd_batched(
+            _lib.dtype_code(Qk), Qk.data_ptr(), Qk.stride(0), Qk.stride(1), Dk.data_ptr(), Dk.stride(0),
+            Dk.stride(1), lengths.data_ptr(), am.data_ptr(), g.data_ptr(), g.stride(0), g.stride(1),
+            dQ.data_ptr(), dD.data_ptr(), Nq, B, Lq, Ld, d, ws.data_ptr(), nbytes,
+            torch.cuda.current_stream().cuda_stream,
+        )
+        _lib.check(rc)
+
+    call()
+    torch.cuda.synchronize()
+    wantQ, wantD = dQ.clone(), dD.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        call()
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dQ.fill_(float("nan"))
+        dD.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(dQ, wantQ) and torch.equal(dD, wantD)
+        call()  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(dQ, wantQ) and torch.equal(dD, wantD)
