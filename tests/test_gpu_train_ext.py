@@ -321,3 +321,69 @@ def test_bwd_graph_capture_replays():
         call()  # eager work between replays
         torch.cuda.synchronize()
         assert torch.equal(dQ, wantQ) and torch.equal(dD, wantD)
+
+
+def test_bwd_forked_from_two_host_threads():
+    """Two host threads, each on its own stream with its own outputs and
+    workspace, run the forked backward (dD of 2^24 bytes or more) at the same
+    time, several times over: the library's shared second stream and its
+    fork/join events must keep every call's dQ ordered before its own stream's
+    later work. Each result must equal the serial one byte for byte."""
+    import threading
+
+    from flash_maxsim_amd import _lib
+
+    Nq, B, Lq, Ld, d = 1, 300, 32, 256, 128
+    gen = torch.Generator().manual_seed(2100)
+    Qk = _prep(torch.randn(Nq, Lq, d, generator=gen).to(torch.float16).to(DEV), torch.float16)
+    Dk = _prep(torch.randn(B, Ld, d, generator=gen).to(torch.float16).to(DEV), torch.float16)
+    lengths = torch.randint(1, Ld + 1, (B,), generator=gen, dtype=torch.int32).to(DEV)
+    _, am = _launch_fwd(Qk, Dk, lengths, Nq, B, Lq, Ld, d, True, True)
+    grads = [torch.randn(Nq, B, generator=gen).to(DEV) for _ in range(2)]
+    lib = _lib.load()
+    nbytes = lib.fmx_bwd_batched_workspace_bytes(Nq, B, Lq, Ld, d)
+
+    def call(g, dQ, dD, ws, stream):
+        rc = lib.fmx_bwd_batched(
+            _lib.dtype_code(Qk), Qk.data_ptr(), Qk.stride(0), Qk.stride(1), Dk.data_ptr(), Dk.stride(0),
+            Dk.stride(1), lengths.data_ptr(), am.data_ptr(), g.data_ptr(), g.stride(0), g.stride(1),
+            dQ.data_ptr(), dD.data_ptr(), Nq, B, Lq, Ld, d, ws.data_ptr(), nbytes, stream.cuda_stream,
+        )
+        _lib.check(rc)
+
+    bufs = [(torch.empty(Nq, Lq, d, dtype=torch.float16, device=DEV),
+             torch.empty(B, Ld, d, dtype=torch.float16, device=DEV),
+             torch.empty(nbytes, dtype=torch.uint8, device=DEV)) for _ in range(2)]
+    main = torch.cuda.current_stream()
+    want = []
+    for i in range(2):
+        call(grads[i], *bufs[i], main)
+        torch.cuda.synchronize()
+        want.append((bufs[i][0].clone(), bufs[i][1].clone()))
+    streams = [torch.cuda.Stream() for _ in range(2)]
+    got = [[], []]
+    errors = []
+
+    def worker(i):
+        try:
+            torch.cuda.set_device(0)
+            with torch.cuda.stream(streams[i]):
+                for _ in range(6):
+                    bufs[i][0].fill_(float("nan"))
+                    bufs[i][1].fill_(float("nan"))
+                    call(grads[i], *bufs[i], streams[i])
+                    got[i].append((bufs[i][0].clone(), bufs[i][1].clone()))  # ordered after the join
+        except Exception as e:  # reported on the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    for i in range(2):
+        assert len(got[i]) == 6
+        for gQ, gD in got[i]:
+            assert torch.equal(gQ, want[i][0]) and torch.equal(gD, want[i][1])
