@@ -76,6 +76,72 @@ __device__ __forceinline__ void load8(const void* row, int k0, int d, bool vec, 
   }
 }
 
+// fp16 sources keep their loaded halves packed: the row scan runs on pairs
+// and the subtraction x - lo reads each half directly, so no fp32 copy of the
+// row is formed (one conversion per element fewer).
+// Packed NaN-propagating minimum / maximum of three fp16 pairs (as the fp32
+// minimum and maximum: NaN wins, -0 < +0).
+__device__ __forceinline__ uint32_t pk_min3(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t r;
+  asm("v_pk_minimum3_f16 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ uint32_t pk_max3(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t r;
+  asm("v_pk_maximum3_f16 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+// Minimum (maximum) over the eight halves of w, as fp32: three packed steps
+// (the last pairs each half with the other) and one conversion.
+__device__ __forceinline__ float min8_f16(const uint32_t (&w)[4]) {
+  uint32_t m = pk_min3(w[0], w[1], w[2]);
+  m = pk_min3(m, w[3], w[3]);
+  uint32_t r;
+  asm("v_pk_minimum3_f16 %0, %1, %1, %1 op_sel:[0,1,0] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(m));
+  return half_bits_to_float(r & 0xffffu);
+}
+__device__ __forceinline__ float max8_f16(const uint32_t (&w)[4]) {
+  uint32_t m = pk_max3(w[0], w[1], w[2]);
+  m = pk_max3(m, w[3], w[3]);
+  uint32_t r;
+  asm("v_pk_maximum3_f16 %0, %1, %1, %1 op_sel:[0,1,0] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(m));
+  return half_bits_to_float(r & 0xffffu);
+}
+// RN(x - lo) for the fp16 value in half H of w, x widened exactly inside a
+// mixed-precision fma (x * 1 + (-lo), one rounding): the same fp32 value as
+// converting x and subtracting.
+template <int H>
+__device__ __forceinline__ float sub_f16(uint32_t w, float nlo) {
+  float r;
+  if constexpr (H == 0) {
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(nlo));
+  } else {
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(nlo));
+  }
+  return r;
+}
+// Eight fp16 elements k0..k0+7 of a row as four packed words; halves at or
+// past d repeat element k0 (k0 < d), which leaves the row's min and max as
+// they are.
+template <bool NT>
+__device__ __forceinline__ void load8_f16(const void* row, int k0, int d, bool vec, uint32_t (&w)[4]) {
+  const uint16_t* r = static_cast<const uint16_t*>(row);
+  if (vec && k0 + 8 <= d) {
+    const u32x4_t* p = reinterpret_cast<const u32x4_t*>(r + k0);
+    const u32x4_t v = NT ? __builtin_nontemporal_load(p) : *p;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = v[i];
+  } else if (k0 < d) {
+    const uint32_t first = r[k0];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lo = k0 + 2 * i < d ? (uint32_t)r[k0 + 2 * i] : first;
+      const uint32_t hi = k0 + 2 * i + 1 < d ? (uint32_t)r[k0 + 2 * i + 1] : first;
+      w[i] = lo | (hi << 16);
+    }
+  }
+}
+
 // Correctly rounded a / b from y = RN(1 / b). q0 = RN(a * y) can be 2 ulp
 // off (y and the product each round by up to 2^-24 relative); one fma
 // correction, q1 = RN(q0 + RN(a - b*q0) * y), brings it within 1 ulp, after
@@ -154,15 +220,21 @@ __global__ void __launch_bounds__(256) quantize_kernel(QuantArgs a) {
     // zero rows up to the next multiple of 4.
     const int64_t jend = packed ? ((len + 3) & ~(int64_t)3) : a.Ld;
     const int64_t obase = packed ? 4 * a.tok_group[b] : b * a.Ld;
-    float x[R][CPL][8];
+    constexpr bool PK = SRC == 0;  // packed fp16 halves (above)
+    float x[PK ? 1 : R][CPL][8];
+    uint32_t xh[PK ? R : 1][CPL][4];
 #pragma unroll
     for (int k = 0; k < R; ++k) {
       const int64_t j = jbase + k;
       if (j < jend && j < len) {
         const char* src = static_cast<const char*>(a.src) + (b * a.s_stride_b + j * a.s_stride_l) * a.esz;
 #pragma unroll
-        for (int cc = 0; cc < CPL; ++cc)
-          load8<SRC, (SRC != 2 && LPR >= 8)>(src, (cc * LPR + lane_in_row) * 8, a.d, a.vec != 0, x[k][cc]);
+        for (int cc = 0; cc < CPL; ++cc) {
+          if constexpr (PK)
+            load8_f16<(LPR >= 8)>(src, (cc * LPR + lane_in_row) * 8, a.d, a.vec != 0, xh[k][cc]);
+          else
+            load8<SRC, (SRC != 2 && LPR >= 8)>(src, (cc * LPR + lane_in_row) * 8, a.d, a.vec != 0, x[k][cc]);
+        }
       }
     }
 #pragma unroll
@@ -188,7 +260,12 @@ __global__ void __launch_bounds__(256) quantize_kernel(QuantArgs a) {
 #pragma unroll
       for (int cc = 0; cc < CPL; ++cc) {
         const int k0 = (cc * LPR + lane_in_row) * 8;
-        if (k0 + 8 <= a.d) {
+        if constexpr (PK) {
+          if (k0 < a.d) {
+            lo = mm<false>(lo, min8_f16(xh[k][cc]));
+            hi = mm<true>(hi, max8_f16(xh[k][cc]));
+          }
+        } else if (k0 + 8 <= a.d) {
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
             lo = mm<false>(lo, x[k][cc][i]);
@@ -211,9 +288,18 @@ __global__ void __launch_bounds__(256) quantize_kernel(QuantArgs a) {
         const int k0 = (cc * LPR + lane_in_row) * 8;
         if (k0 >= a.d) continue;
         uint32_t w[2] = {0u, 0u};
+        if constexpr (PK) {
+          const float nlo = -lo;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          w[i >> 2] = cvt_u8_rne(div_rn<SRC == 0>(x[k][cc][i] - lo, step, rstep), i & 3, w[i >> 2]);
+          for (int i = 0; i < 8; ++i) {
+            const float av = (i & 1) ? sub_f16<1>(xh[k][cc][i >> 1], nlo) : sub_f16<0>(xh[k][cc][i >> 1], nlo);
+            w[i >> 2] = cvt_u8_rne(div_rn<true>(av, step, rstep), i & 3, w[i >> 2]);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            w[i >> 2] = cvt_u8_rne(div_rn<SRC == 0>(x[k][cc][i] - lo, step, rstep), i & 3, w[i >> 2]);
+          }
         }
         if (a.vec && k0 + 8 <= a.d) {
           // non-temporal: the codes are read by a later scoring call, not by

@@ -339,3 +339,33 @@ def test_packed_doc_ids_out_of_range_not_written():
     keep[lost] = False
     assert torch.all(scores.cpu()[~keep] == 7.0)
     assert torch.equal(scores.cpu()[keep], want.cpu()[keep])
+
+
+@pytest.mark.parametrize("d", [128, 100, 16, 8, 7, 1])
+def test_quantize_fp16_special_values_bitwise(d):
+    """fp16 sources take the packed path (row min/max on pairs of halves, x - min
+    formed from each half by a mixed-precision fma): rows with fp16 subnormals,
+    +-65504, values one ulp apart and the extremes in either half of a word or
+    in a partial last chunk must quantise bit for bit as the reference's torch
+    formula does on the CPU."""
+    gen = torch.Generator().manual_seed(2200 + d)
+    rows = 64
+    x = (torch.randn(rows, d, generator=gen) * 4).to(torch.float16)
+    tiny = torch.tensor([2.0**-24, 3 * 2.0**-24, 2.0**-14, -(2.0**-24), -1023 * 2.0**-24]).to(torch.float16)
+    for r in range(rows):
+        k = r % d
+        if r % 4 == 0:
+            x[r] = tiny[torch.randint(0, len(tiny), (d,), generator=gen)]
+        elif r % 4 == 1:
+            x[r, k] = 65504.0 if r % 8 == 1 else -65504.0
+        elif r % 4 == 2:
+            base = x[r, 0].view(torch.int16)
+            x[r] = (base + torch.randint(-2, 3, (d,), generator=gen, dtype=torch.int16)).view(torch.float16)
+        else:
+            x[r, k] = x[r].float().max().half() * 2 + 1  # the maximum at a rotating position
+    x3 = x.reshape(8, 8, d)
+    got = fm.quantize_int8(x3.to(DEV))
+    want = fm.quantize_int8(x3)  # torch formula on the CPU
+    np.testing.assert_array_equal(got[0].cpu().numpy(), want[0].numpy())
+    np.testing.assert_array_equal(_bits(got[1]), _bits(want[1]))
+    np.testing.assert_array_equal(_bits(got[2]), _bits(want[2]))
