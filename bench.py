@@ -318,16 +318,20 @@ def build(name: str, rotate: int, doc_align: int = 4) -> Workload:
         Q = sim((Lq, d), 51, f16)
         Dh = sim((B, Ld, d), 52, f16)
         Qd = Q.to(dev).requires_grad_(True)
-        Dd = Dh.to(dev).requires_grad_(True)
+        Dds = [D.requires_grad_(True) for D in _copies(Dh.to(dev), rotate)]
 
-        def step():
-            s = fm.flash_maxsim_train(Qd, Dd)
-            s.sum().backward()
-            Qd.grad = None
-            Dd.grad = None
+        def make_step(Dd):
+            def step():
+                s = fm.flash_maxsim_train(Qd, Dd)
+                s.sum().backward()
+                Qd.grad = None
+                Dd.grad = None
+            return step
 
         cfg = {"workload": f"train fwd+bwd flash_maxsim_train Q[{Lq},{d}] x D[{B},{Ld},{d}] fp16", "B": B,
                "Lq": Lq, "Ld": Ld, "d": d}
+        if rotate > 1:
+            cfg["rotated_doc_copies"] = len(Dds)
         # D read by the forward + dD written + the B*Lq rows of D gathered for dQ
         # + argmax written and read back (Q, dQ and scores are < 1 MB).
         roof = {"bound": "hbm", "amount": 2 * B * Ld * d * 2 + B * Lq * d * 2 + B * Lq * 4 * 2, "unit": "GB/s",
@@ -341,7 +345,7 @@ def build(name: str, rotate: int, doc_align: int = 4) -> Workload:
             Qc.grad = None
             Dc.grad = None
 
-        return Workload(cfg, [step], B, "docs/s", roof, cpu, n,
+        return Workload(cfg, [make_step(D) for D in Dds], B, "docs/s", roof, cpu, n,
                         f"maxsim_naive fp32 forward + autograd backward over the first {n} docs")
 
     if name == "copy":
